@@ -1,0 +1,80 @@
+/*
+ * libpyrite_hip.so -- MI355X (gfx950) GGML dequantize x matvec, C ABI.
+ *
+ * Part 1 is a drop-in for the reference's native kernel library: the same three
+ * symbols, signatures, argument meaning and return codes as
+ * pyrite/kernels/native.c, so pyrite/kernels/native.py can load this library
+ * instead of compiling native.c (see INTEGRATION.md for the binding).
+ *
+ * Part 2 is device-resident: weights are GGUF block bytes uploaded verbatim
+ * into HBM, activations and outputs are fp32 device buffers, and work is
+ * queued on a caller-supplied HIP stream (NULL = the per-thread default
+ * stream).  These replace the per-call host round trips at the reference's
+ * dispatch sites (pyrite/executor.py:481-594, 757-793, 852-875).
+ *
+ * Return codes (pyrite/kernels/native.c:496-525, 562-566):
+ *    0  success
+ *   -1  unknown GGML type id
+ *   -2  bad geometry: rows == 0, cols == 0, cols not a multiple of the block
+ *       size, size overflow, or a shape the device kernels do not support
+ *   -3  NULL pointer, data_len != rows * row_bytes, or a misaligned buffer
+ *   -4  HIP runtime error (message from pyrite_hip_last_error())
+ * Types: F32 F16 Q4_0 Q4_1 Q5_0 Q5_1 Q8_0 Q8_1 Q2_K Q3_K Q4_K Q5_K Q6_K
+ *        IQ4_NL IQ4_XS I8 I16 I32 I64 F64 BF16 (ids 0 1 2 3 6 7 8 9 10 11 12
+ *        13 14 20 23 24 25 26 27 28 30), reported in that order.
+ */
+#ifndef PYRITE_HIP_H
+#define PYRITE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------ 1. drop-in */
+
+/* Replaces pyrite_native_types (pyrite/kernels/native.c:484-494): ids == NULL
+ * returns the count (21); otherwise copies min(count, capacity) ids in table
+ * order and returns how many were written. */
+int pyrite_native_types(int *ids, size_t capacity);
+
+/* Replaces pyrite_matvec (pyrite/kernels/native.c:518-555).  data: host bytes
+ * of rows x row_bytes GGUF blocks (borrowed for the call); x: host double[cols];
+ * out: host double[rows].  Runs on the GPU in fp64 over the exact fp64
+ * weights, so out differs from the reference only by fp64 summation order. */
+int pyrite_matvec(int type_id, const uint8_t *data, size_t data_len,
+                  const double *x, double *out, size_t rows, size_t cols);
+
+/* Replaces pyrite_dequantize_rows (pyrite/kernels/native.c:557-576).  out is
+ * host double[rows * cols], row-major; values are bit-identical to the
+ * reference (computed in fp64 on the GPU). */
+int pyrite_dequantize_rows(int type_id, const uint8_t *data, size_t data_len,
+                           double *out, size_t rows, size_t cols);
+
+/* ------------------------------------------------------------ 2. device-resident */
+
+/* Last error message of the calling thread ("" if none). */
+const char *pyrite_hip_last_error(void);
+
+/* y[b * ldy + r] = sum_c dequant(w)[r][c] * x[b * ldx + c] for b < batch.
+ * w: device bytes (rows x row_bytes, any alignment); x, y: device fp32.
+ * Quantized types need x 16-byte aligned and ldx % 4 == 0.  Replaces the
+ * native matvec calls of pyrite/executor.py:481-509 and 545-594 (there with
+ * batch 1 and fp64 host buffers). */
+int pyrite_dev_matvec(int type_id, const void *w, size_t w_len, size_t rows, size_t cols,
+                      const float *x, size_t ldx, float *y, size_t ldy, size_t batch,
+                      void *stream);
+
+/* Exact dequantization into device memory: fp32 when out_f64 == 0 (equal to
+ * (float) of the reference double) or fp64 (bit-identical).  Replaces
+ * pyrite_dequantize_rows at pyrite/executor.py:470-475 (embedding rows). */
+int pyrite_dev_dequantize(int type_id, const void *w, size_t w_len, size_t rows, size_t cols,
+                          void *out, int out_f64, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PYRITE_HIP_H */

@@ -1,0 +1,190 @@
+// Shared device helpers for the gfx950 GGML kernels.
+//
+// Weight bytes are GGUF block payloads uploaded verbatim into HBM.  Several
+// block sizes (18, 22, 34, 110, 210 bytes) leave blocks only 2-byte aligned, so
+// the loaders below read whole, dword-aligned words and realign them with
+// v_alignbyte_b32.  Every dword a loader touches contains at least one byte of
+// the requested span, so no load leaves the caller's buffer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace pyrite {
+
+// ---------------------------------------------------------------- type table
+// Ids, block sizes and bytes per block of the 21 supported GGML types, in the
+// order of the reference table (pyrite/kernels/native.c:451-473).
+enum TypeId : int {
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8,
+    T_Q8_1 = 9, T_Q2_K = 10, T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14,
+    T_IQ4_NL = 20, T_IQ4_XS = 23, T_I8 = 24, T_I16 = 25, T_I32 = 26, T_I64 = 27,
+    T_F64 = 28, T_BF16 = 30,
+};
+
+template <int T> struct Geo;
+#define PYRITE_GEO(T, BS, BPB) \
+    template <> struct Geo<T> { static constexpr int bs = BS; static constexpr int bpb = BPB; };
+PYRITE_GEO(T_F32, 1, 4)
+PYRITE_GEO(T_F16, 1, 2)
+PYRITE_GEO(T_Q4_0, 32, 18)
+PYRITE_GEO(T_Q4_1, 32, 20)
+PYRITE_GEO(T_Q5_0, 32, 22)
+PYRITE_GEO(T_Q5_1, 32, 24)
+PYRITE_GEO(T_Q8_0, 32, 34)
+PYRITE_GEO(T_Q8_1, 32, 36)
+PYRITE_GEO(T_Q2_K, 256, 84)
+PYRITE_GEO(T_Q3_K, 256, 110)
+PYRITE_GEO(T_Q4_K, 256, 144)
+PYRITE_GEO(T_Q5_K, 256, 176)
+PYRITE_GEO(T_Q6_K, 256, 210)
+PYRITE_GEO(T_IQ4_NL, 32, 18)
+PYRITE_GEO(T_IQ4_XS, 256, 136)
+PYRITE_GEO(T_I8, 1, 1)
+PYRITE_GEO(T_I16, 1, 2)
+PYRITE_GEO(T_I32, 1, 4)
+PYRITE_GEO(T_I64, 1, 8)
+PYRITE_GEO(T_F64, 1, 8)
+PYRITE_GEO(T_BF16, 1, 2)
+#undef PYRITE_GEO
+
+// ---------------------------------------------------------------- scalars
+__device__ __forceinline__ float half_bits_to_float(uint32_t h16) {
+    // v_cvt_f32_f16: exact for every binary16 input, subnormals included
+    // (kernels run with f16 denormals enabled, the gfx9 default).
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)(h16 & 0xFFFFu));
+}
+
+__device__ __forceinline__ double half_bits_to_double(uint32_t h16) {
+    return (double)half_bits_to_float(h16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t b16) {
+    return __uint_as_float((b16 & 0xFFFFu) << 16);
+}
+
+// ---------------------------------------------------------------- loads
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t* p) {
+    return *reinterpret_cast<const uint32_t*>(p);
+}
+
+// Four dwords from a 4-byte-aligned address: one global_load_dwordx4.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+__device__ __forceinline__ void ld_a4x4(const uint8_t* p, uint32_t (&w)[4]) {
+    u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(p);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+}
+
+// N dwords holding bytes [p, p + NB) (NB <= 4N), p of any alignment when !AL.
+// Aligned case: plain dword loads (merged into dwordx4 where possible).
+// Unaligned case: dword-aligned loads whose addresses are clamped to the last
+// dword that still overlaps the span, then v_alignbyte_b32 realigns them; the
+// bytes past NB in the last output word are unspecified.
+template <int NB, bool AL>
+__device__ __forceinline__ void ld_span(const uint8_t* p, uint32_t (&w)[(NB + 3) / 4]) {
+    constexpr int N = (NB + 3) / 4;
+    if constexpr (AL) {
+#pragma unroll
+        for (int k = 0; k < N; k += 4) {
+            if constexpr (true) {
+                if (k + 4 <= N) {
+                    uint32_t t[4];
+                    ld_a4x4(p + 4 * k, t);
+                    w[k] = t[0]; w[k + 1] = t[1]; w[k + 2] = t[2]; w[k + 3] = t[3];
+                } else {
+#pragma unroll
+                    for (int j = k; j < N; ++j) w[j] = ld_u32(p + 4 * j);
+                }
+            }
+        }
+    } else {
+        // base = p rounded down to a dword (pointer arithmetic keeps the global
+        // address space); dword k of the span window is safe to read unclamped
+        // while 4k <= NB - 4, because the last dword overlapping the span starts
+        // at ((s + NB - 1) & ~3) >= NB - 4.
+        const uint32_t s = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+        const uint8_t* base = p - s;
+        const uint32_t last = (s + NB - 1) & ~3u;
+        // dwords [0, NX4) come from dwordx4 loads that lie wholly inside the window
+        constexpr int NX4 = (NB >= 16) ? ((NB - 16) / 16 + 1) * 4 : 0;
+        uint32_t t[N + 1];
+#pragma unroll
+        for (int k = 0; k < NX4; k += 4) {
+            uint32_t v[4];
+            ld_a4x4(base + 4 * k, v);
+            t[k] = v[0]; t[k + 1] = v[1]; t[k + 2] = v[2]; t[k + 3] = v[3];
+        }
+#pragma unroll
+        for (int k = NX4; k <= N; ++k) {
+            if (4 * k + 4 <= NB) {
+                t[k] = ld_u32(base + 4 * k);
+            } else {
+                const uint32_t off = (4u * k < last) ? 4u * k : last;
+                t[k] = ld_u32(base + off);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < N; ++k) w[k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], s);
+    }
+}
+
+// ---------------------------------------------------------------- x access
+__device__ __forceinline__ float4 ld_x4(const float* p) {
+    return *reinterpret_cast<const float4*>(p);
+}
+
+// Bit operations whose result the compiler cannot see through.  Code words are
+// built with these so that the byte conversions below stay single
+// v_cvt_f32_ubyte{0..3} instructions; with a visible mask the compiler turns
+// each byte into v_bfe_u32 + v_cvt_f32_ubyte0 (two instructions per weight).
+__device__ __forceinline__ uint32_t oand(uint32_t v, uint32_t m) {
+    uint32_t r;
+    asm("v_and_b32 %0, %1, %2" : "=v"(r) : "s"(m), "v"(v));
+    return r;
+}
+// (v & m) | c
+__device__ __forceinline__ uint32_t oandor(uint32_t v, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(v), "s"(m), "v"(c));
+    return r;
+}
+// (hi & mask) | (lo & ~mask)
+__device__ __forceinline__ uint32_t obfi(uint32_t mask, uint32_t hi, uint32_t lo) {
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask), "v"(hi), "v"(lo));
+    return r;
+}
+
+// sum_i ubyte_i(v) * x_i + acc  (v_cvt_f32_ubyte{0..3} + v_fmac)
+__device__ __forceinline__ float dot_ub4(uint32_t v, float4 x, float acc) {
+    acc = fmaf((float)(v & 0xFFu), x.x, acc);
+    acc = fmaf((float)((v >> 8) & 0xFFu), x.y, acc);
+    acc = fmaf((float)((v >> 16) & 0xFFu), x.z, acc);
+    acc = fmaf((float)(v >> 24), x.w, acc);
+    return acc;
+}
+
+// IQ4 codebook (kvalues_iq4nl, pyrite/kernels/native.c:347-349) biased by +128
+// so every entry is an unsigned byte: 1 24 45 63 79 93 106 118 129 141 153 166
+// 181 197 217 241.
+constexpr uint32_t IQ4B_0 = 0x3F2D1801u, IQ4B_1 = 0x766A5D4Fu;
+constexpr uint32_t IQ4B_2 = 0xA6998D81u, IQ4B_3 = 0xF1D9C5B5u;
+
+// Look up four nibbles (one per byte, values 0..15) in the biased codebook.
+__device__ __forceinline__ uint32_t iq4_lut4(uint32_t n) {
+    const uint32_t sel = n & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(IQ4B_1, IQ4B_0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(IQ4B_3, IQ4B_2, sel);
+    // selector 0x0C yields 0x00 and 0x0D yields 0xFF: a byte mask from bit 3
+    const uint32_t msel = 0x0C0C0C0Cu | ((n >> 3) & 0x01010101u);
+    const uint32_t mask = __builtin_amdgcn_perm(0u, 0u, msel);
+    return obfi(mask, hi, lo);
+}
+
+// Spread the low 4 bits of v to bit 0 of each byte.
+__device__ __forceinline__ uint32_t spread4(uint32_t v) {
+    return ((v & 0xFu) * 0x00204081u) & 0x01010101u;
+}
+
+}  // namespace pyrite

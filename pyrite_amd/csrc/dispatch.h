@@ -1,0 +1,64 @@
+// Host-side type geometry and launchers shared by the C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace pyrite {
+
+struct TypeGeo {
+    bool valid;
+    int bs;   // elements per block
+    int bpb;  // bytes per block
+};
+
+// The 21 GGML types of the reference table, in table order
+// (pyrite/kernels/native.c:451-473).
+constexpr int kTypeIds[21] = {0, 1, 2, 3, 6, 7, 8, 9, 10, 11, 12, 13, 14, 20, 23, 24, 25, 26, 27, 28, 30};
+
+inline TypeGeo type_geo(int id) {
+    switch (id) {
+    case 0: return {true, 1, 4};
+    case 1: return {true, 1, 2};
+    case 2: return {true, 32, 18};
+    case 3: return {true, 32, 20};
+    case 6: return {true, 32, 22};
+    case 7: return {true, 32, 24};
+    case 8: return {true, 32, 34};
+    case 9: return {true, 32, 36};
+    case 10: return {true, 256, 84};
+    case 11: return {true, 256, 110};
+    case 12: return {true, 256, 144};
+    case 13: return {true, 256, 176};
+    case 14: return {true, 256, 210};
+    case 20: return {true, 32, 18};
+    case 23: return {true, 256, 136};
+    case 24: return {true, 1, 1};
+    case 25: return {true, 1, 2};
+    case 26: return {true, 1, 4};
+    case 27: return {true, 1, 8};
+    case 28: return {true, 1, 8};
+    case 30: return {true, 1, 2};
+    default: return {false, 0, 0};
+    }
+}
+
+#define PYRITE_FOR_EACH_TYPE(X)                                                                     \
+    X(0) X(1) X(2) X(3) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(20) X(23) X(24) X(25) \
+    X(26) X(27) X(28) X(30)
+
+// matvec.hip: Y[b][r] = sum_c W[r][c] X[b][c] in fp32, any batch (chunked by 8).
+// Returns 0, -1 (type), -2 (geometry), -3 (pointer/length/alignment), -4 (launch).
+int matvec_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* X, size_t ldx,
+                  float* Y, size_t ldy, size_t batch, hipStream_t stream);
+
+// dequant.hip: fp64 matvec over exact fp64 weights (the host drop-in path).
+int matvec64_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const double* X,
+                    double* Y, hipStream_t stream);
+
+// dequant.hip: exact dequantization into fp32 (out_f64 == 0) or fp64.
+int dequant_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, void* out, int out_f64,
+                   hipStream_t stream);
+
+}  // namespace pyrite

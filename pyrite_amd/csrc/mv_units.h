@@ -1,0 +1,453 @@
+// Per-type "unit" decoders for the fp32 dequant-matvec (VALU path).
+//
+// A unit is the slice of one block a lane owns: 32 weights (one whole block)
+// for the 32-element formats, 64 weights (a quarter super-block) for the
+// 256-element formats, 4 elements for the plain types.  A unit is decoded for
+// R rows that share the same columns, against B activation vectors, with the
+// block scale factored out of the inner loop:
+//     sum_i (d*sc*q_i - dmin*m) x_i = d*sc * sum_i q_i x_i - dmin*m * sum_i x_i
+// q_i are converted with v_cvt_f32_ubyte{0..3}; sum_i x_i over every 16
+// columns is precomputed per workgroup in LDS (xs16).  Element order inside a
+// unit follows each block layout (pyrite/kernels/native.c:129-437).
+#pragma once
+
+#include "common.h"
+
+namespace pyrite {
+
+struct XView {
+    const float* x;     // activations of column 0 of this block, batch 0
+    size_t ldx;         // floats between batch rows
+    const float* xs16;  // LDS: sum of each 16 columns, batch 0, from column 0 of this block
+    int ld16;           // floats between batch rows in xs16
+};
+
+// sum over 16 consecutive columns of u32 codes (4 per dword) against x
+template <int NW>
+__device__ __forceinline__ float dot_run(const uint32_t (&c)[NW], const float* x) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < NW; ++k) s = dot_ub4(c[k], ld_x4(x + 4 * k), s);
+    return s;
+}
+
+template <int T> struct Unit;
+
+// ------------------------------------------------------------------ Q4_K
+// unit c (0..3): qs[32c, 32c+32); low nibbles -> columns 64c+l (sub-block 2c),
+// high nibbles -> 64c+32+l (sub-block 2c+1).  pyrite/kernels/native.c:173-197
+__device__ __forceinline__ void k4_pair_regs(uint32_t s0, uint32_t s1, uint32_t s2, int c,
+                                             float& sc0, float& m0, float& sc1, float& m1) {
+    const uint32_t k = 16u * (c & 1);
+    const uint32_t Ba = (s0 >> k) & 0xFF, Bb = (s0 >> (k + 8)) & 0xFF;
+    const uint32_t Ma = (s1 >> k) & 0xFF, Mb = (s1 >> (k + 8)) & 0xFF;
+    const uint32_t Ca = (s2 >> k) & 0xFF, Cb = (s2 >> (k + 8)) & 0xFF;
+    uint32_t a0, a1, a2, a3;
+    if (c < 2) {
+        a0 = Ba & 63; a1 = Ma & 63; a2 = Bb & 63; a3 = Mb & 63;
+    } else {
+        a0 = (Ca & 15) | ((Ba >> 6) << 4);
+        a1 = (Ca >> 4) | ((Ma >> 6) << 4);
+        a2 = (Cb & 15) | ((Bb >> 6) << 4);
+        a3 = (Cb >> 4) | ((Mb >> 6) << 4);
+    }
+    sc0 = (float)a0; m0 = (float)a1; sc1 = (float)a2; m1 = (float)a3;
+}
+
+template <> struct Unit<T_Q4_K> {
+    static constexpr int P = 4;
+    template <int B, int R, bool AL>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int c, const XView& xv,
+                                               float (&acc)[R][B]) {
+        uint32_t hd[R][4], q[R][8];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ld_span<16, AL>(blk[r], hd[r]);
+            ld_span<32, AL>(blk[r] + 16 + 32 * c, q[r]);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float* x = xv.x + b * xv.ldx + 64 * c;
+            const float* s16 = xv.xs16 + b * xv.ld16 + 4 * c;
+            const float xlo = s16[0] + s16[1], xhi = s16[2] + s16[3];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                uint32_t lo[8], hi[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) { lo[k] = oand(q[r][k], 0x0F0F0F0Fu); hi[k] = oand(q[r][k], 0xF0F0F0F0u); }
+                const float slo = dot_run<8>(lo, x);
+                const float shi = dot_run<8>(hi, x + 32);
+                float sc0, m0, sc1, m1;
+                k4_pair_regs(hd[r][1], hd[r][2], hd[r][3], c, sc0, m0, sc1, m1);
+                const float d = half_bits_to_float(hd[r][0]), dmin = half_bits_to_float(hd[r][0] >> 16);
+                acc[r][b] += d * (sc0 * slo + sc1 * 0.0625f * shi) - dmin * (m0 * xlo + m1 * xhi);
+            }
+        }
+    }
+};
+
+// ------------------------------------------------------------------ Q5_K
+// as Q4_K plus a fifth bit: qh[l] bit 2c (low) / 2c+1 (high).  native.c:410-437
+template <> struct Unit<T_Q5_K> {
+    static constexpr int P = 4;
+    template <int B, int R, bool AL>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int c, const XView& xv,
+                                               float (&acc)[R][B]) {
+        uint32_t hd[R][4], q[R][8], h[R][8];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ld_span<16, AL>(blk[r], hd[r]);
+            ld_span<32, AL>(blk[r] + 16, h[r]);
+            ld_span<32, AL>(blk[r] + 48 + 32 * c, q[r]);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float* x = xv.x + b * xv.ldx + 64 * c;
+            const float* s16 = xv.xs16 + b * xv.ld16 + 4 * c;
+            const float xlo = s16[0] + s16[1], xhi = s16[2] + s16[3];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                uint32_t lo[8], hi[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    lo[k] = oandor(q[r][k], 0x0F0F0F0Fu, ((h[r][k] >> (2 * c)) & 0x01010101u) << 4);
+                    hi[k] = oandor(q[r][k] >> 4, 0x0F0F0F0Fu, ((h[r][k] >> (2 * c + 1)) & 0x01010101u) << 4);
+                }
+                const float slo = dot_run<8>(lo, x);
+                const float shi = dot_run<8>(hi, x + 32);
+                float sc0, m0, sc1, m1;
+                k4_pair_regs(hd[r][1], hd[r][2], hd[r][3], c, sc0, m0, sc1, m1);
+                const float d = half_bits_to_float(hd[r][0]), dmin = half_bits_to_float(hd[r][0] >> 16);
+                acc[r][b] += d * (sc0 * slo + sc1 * shi) - dmin * (m0 * xlo + m1 * xhi);
+            }
+        }
+    }
+};
+
+// ------------------------------------------------------------------ Q6_K
+// unit u = (h, r') = (u >> 1, u & 1): columns 128h + 32g + 16r' + l, g = 0..3,
+// l = 0..15.  ql bytes 64h+16r'+l (g even) and 64h+32+16r'+l (g odd), nibble
+// g >> 1; qh byte 32h+16r'+l bits 2g; scale 8h + 2g + r'.  native.c:199-225
+template <> struct Unit<T_Q6_K> {
+    static constexpr int P = 4;
+    template <int B, int R, bool AL>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XView& xv,
+                                               float (&acc)[R][B]) {
+        const int h = u >> 1, rr = u & 1;
+        uint32_t A[R][4], Bq[R][4], H[R][4], S[R][2], D[R][1];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ld_span<16, AL>(blk[r] + 64 * h + 16 * rr, A[r]);
+            ld_span<16, AL>(blk[r] + 64 * h + 32 + 16 * rr, Bq[r]);
+            ld_span<16, AL>(blk[r] + 128 + 32 * h + 16 * rr, H[r]);
+            ld_span<8, AL>(blk[r] + 192 + 8 * h, S[r]);
+            ld_span<2, AL>(blk[r] + 208, D[r]);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float* x = xv.x + b * xv.ldx + 128 * h + 16 * rr;
+            const float* s16 = xv.xs16 + b * xv.ld16 + 8 * h + rr;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float tot = 0.f;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    uint32_t c[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const uint32_t lq = (g & 1) ? Bq[r][k] : A[r][k];
+                        c[k] = oandor((g & 2) ? (lq >> 4) : lq, 0x0F0F0F0Fu,
+                                      ((H[r][k] >> (2 * g)) & 0x03030303u) << 4);
+                    }
+                    const float sg = dot_run<4>(c, x + 32 * g);
+                    const uint32_t sw = S[r][g >> 1] >> (8 * (rr + 2 * (g & 1)));
+                    const float sc = (float)(int)(int8_t)(sw & 0xFF);
+                    tot += sc * (sg - 32.f * s16[2 * g]);
+                }
+                acc[r][b] += half_bits_to_float(D[r][0]) * tot;
+            }
+        }
+    }
+};
+
+// ------------------------------------------------------------------ Q2_K
+// unit (h, r'): qs bytes 32h+16r'+l hold the 2-bit codes of columns
+// 128h + 32g + 16r' + l at bits 2g; scale byte 8h + 2g + r' (low nibble scale,
+// high nibble min); d, dmin at 80, 82.  native.c:381-408
+template <> struct Unit<T_Q2_K> {
+    static constexpr int P = 4;
+    template <int B, int R, bool AL>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XView& xv,
+                                               float (&acc)[R][B]) {
+        const int h = u >> 1, rr = u & 1;
+        uint32_t Q[R][4], S[R][2], D[R][1];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ld_span<16, AL>(blk[r] + 16 + 32 * h + 16 * rr, Q[r]);
+            ld_span<8, AL>(blk[r] + 8 * h, S[r]);
+            ld_span<4, AL>(blk[r] + 80, D[r]);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float* x = xv.x + b * xv.ldx + 128 * h + 16 * rr;
+            const float* s16 = xv.xs16 + b * xv.ld16 + 8 * h + rr;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float ts = 0.f, tm = 0.f;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    uint32_t c[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) c[k] = oand(Q[r][k] >> (2 * g), 0x03030303u);
+                    const float sg = dot_run<4>(c, x + 32 * g);
+                    const uint32_t sb = (S[r][g >> 1] >> (8 * (rr + 2 * (g & 1)))) & 0xFF;
+                    ts += (float)(sb & 15) * sg;
+                    tm += (float)(sb >> 4) * s16[2 * g];
+                }
+                acc[r][b] += half_bits_to_float(D[r][0]) * ts - half_bits_to_float(D[r][0] >> 16) * tm;
+            }
+        }
+    }
+};
+
+// ------------------------------------------------------------------ Q3_K
+// unit (h, r'): 2-bit codes at qs byte 32h+16r'+l bits 2g, high bit at hmask
+// byte 16r'+l bit 4h+g (clear = subtract 4), 6-bit scale j = 8h+2g+r' from the
+// 12 packed bytes at 96, d at 108.  native.c:129-171
+template <> struct Unit<T_Q3_K> {
+    static constexpr int P = 4;
+    template <int B, int R, bool AL>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XView& xv,
+                                               float (&acc)[R][B]) {
+        const int h = u >> 1, rr = u & 1;
+        uint32_t Q[R][4], M[R][4], S[R][3], D[R][1];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ld_span<16, AL>(blk[r] + 32 + 32 * h + 16 * rr, Q[r]);
+            ld_span<16, AL>(blk[r] + 16 * rr, M[r]);
+            ld_span<12, AL>(blk[r] + 96, S[r]);
+            ld_span<2, AL>(blk[r] + 108, D[r]);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float* x = xv.x + b * xv.ldx + 128 * h + 16 * rr;
+            const float* s16 = xv.xs16 + b * xv.ld16 + 8 * h + rr;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float tot = 0.f;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    uint32_t c[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        c[k] = oandor(Q[r][k] >> (2 * g), 0x03030303u,
+                                      ((M[r][k] >> (4 * h + g)) & 0x01010101u) << 2);
+                    const float sg = dot_run<4>(c, x + 32 * g);
+                    // j = 8h + 2g + r': low nibble from byte 2g + r' (h selects the nibble),
+                    // top two bits from byte 8 + (2g + r') % 4 at bit 2 * (2h + g / 2)
+                    const uint32_t lb = (S[r][g >> 1] >> (8 * (rr + 2 * (g & 1)))) & 0xFF;
+                    const uint32_t low4 = h ? (lb >> 4) : (lb & 15);
+                    const uint32_t hb = (S[r][2] >> (8 * ((2 * g + rr) & 3))) & 0xFF;
+                    const uint32_t hi2 = (hb >> (2 * (2 * h + (g >> 1)))) & 3;
+                    const float sc = (float)(int)(low4 | (hi2 << 4)) - 32.f;
+                    tot += sc * (sg - 4.f * s16[2 * g]);
+                }
+                acc[r][b] += half_bits_to_float(D[r][0]) * tot;
+            }
+        }
+    }
+};
+
+// ------------------------------------------------------------------ IQ4_XS
+// unit u: sub-blocks 2u and 2u+1; qs[16 ib + j] low nibble -> column 32ib + j,
+// high -> 32ib + 16 + j; 6-bit scale ls from scales_l / scales_h, value
+// d*(ls-32)*K[n].  native.c:364-379
+template <> struct Unit<T_IQ4_XS> {
+    static constexpr int P = 4;
+    template <int B, int R, bool AL>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XView& xv,
+                                               float (&acc)[R][B]) {
+        uint32_t hd[R][2], q[R][8];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            ld_span<8, AL>(blk[r], hd[r]);
+            ld_span<32, AL>(blk[r] + 8 + 32 * u, q[r]);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float* x = xv.x + b * xv.ldx + 64 * u;
+            const float* s16 = xv.xs16 + b * xv.ld16 + 4 * u;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const uint32_t sl = (hd[r][1] >> (8 * u)) & 0xFF;
+                const uint32_t sh = hd[r][0] >> 16;
+                float tot = 0.f;
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    const int ib = 2 * u + s;
+                    const uint32_t ls = ((sl >> (4 * s)) & 15) | (((sh >> (2 * ib)) & 3u) << 4);
+                    uint32_t lo[4], hi[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        lo[k] = iq4_lut4(q[r][4 * s + k] & 0x0F0F0F0Fu);
+                        hi[k] = iq4_lut4((q[r][4 * s + k] >> 4) & 0x0F0F0F0Fu);
+                    }
+                    const float sv = dot_run<4>(lo, x + 32 * s) + dot_run<4>(hi, x + 32 * s + 16);
+                    const float xs = s16[2 * s] + s16[2 * s + 1];
+                    tot += ((float)(int)ls - 32.f) * (sv - 128.f * xs);
+                }
+                acc[r][b] += half_bits_to_float(hd[r][0]) * tot;
+            }
+        }
+    }
+};
+
+// ------------------------------------------------------------------ 32-element blocks
+// One unit per block.  NB = bytes of the block, OFF = byte offset of qs[0].
+template <int T> struct Small;
+template <> struct Small<T_Q4_0> { static constexpr int NB = 18; };
+template <> struct Small<T_Q4_1> { static constexpr int NB = 20; };
+template <> struct Small<T_Q5_0> { static constexpr int NB = 22; };
+template <> struct Small<T_Q5_1> { static constexpr int NB = 24; };
+template <> struct Small<T_Q8_0> { static constexpr int NB = 34; };
+template <> struct Small<T_Q8_1> { static constexpr int NB = 36; };
+template <> struct Small<T_IQ4_NL> { static constexpr int NB = 18; };
+
+// dword k of a byte stream that starts `off` (even) bytes into w[]
+template <int N>
+__device__ __forceinline__ uint32_t at_off(const uint32_t (&w)[N], int k, int off) {
+    const int i = off / 4 + k;
+    return (off & 2) ? __builtin_amdgcn_alignbyte(w[i + 1], w[i], 2u) : w[i];
+}
+
+#define PYRITE_SMALL_UNIT(T)                                                                         \
+    template <> struct Unit<T> {                                                                     \
+        static constexpr int P = 1;                                                                  \
+        static constexpr int NB = Small<T>::NB;                                                      \
+        template <int B, int R, bool AL>                                                             \
+        __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int, const XView& xv, \
+                                                   float (&acc)[R][B]) {                             \
+            uint32_t w[R][(NB + 3) / 4];                                                             \
+            _Pragma("unroll") for (int r = 0; r < R; ++r) ld_span<NB, AL>(blk[r], w[r]);              \
+            _Pragma("unroll") for (int b = 0; b < B; ++b) {                                          \
+                const float* x = xv.x + b * xv.ldx;                                                  \
+                const float* s16 = xv.xs16 + b * xv.ld16;                                            \
+                const float xs = s16[0] + s16[1];                                                    \
+                _Pragma("unroll") for (int r = 0; r < R; ++r) acc[r][b] += small_dot<T>(w[r], x, xs); \
+            }                                                                                        \
+        }                                                                                            \
+    };
+
+template <int T, int N>
+__device__ __forceinline__ float small_dot(const uint32_t (&w)[N], const float* x, float xs);
+
+// Q4_0: d | qs[16]; d * (q - 8).  native.c:281-288
+template <>
+__device__ __forceinline__ float small_dot<T_Q4_0, 5>(const uint32_t (&w)[5], const float* x, float xs) {
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t v = at_off(w, k, 2);
+        lo[k] = oand(v, 0x0F0F0F0Fu);
+        hi[k] = oand(v, 0xF0F0F0F0u);
+    }
+    const float s = dot_run<4>(lo, x) + 0.0625f * dot_run<4>(hi, x + 16);
+    return half_bits_to_float(w[0]) * (s - 8.f * xs);
+}
+// IQ4_NL: d | qs[16]; d * K[n].  native.c:351-358
+template <>
+__device__ __forceinline__ float small_dot<T_IQ4_NL, 5>(const uint32_t (&w)[5], const float* x, float xs) {
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t v = at_off(w, k, 2);
+        lo[k] = iq4_lut4(v & 0x0F0F0F0Fu);
+        hi[k] = iq4_lut4((v >> 4) & 0x0F0F0F0Fu);
+    }
+    const float s = dot_run<4>(lo, x) + dot_run<4>(hi, x + 16);
+    return half_bits_to_float(w[0]) * (s - 128.f * xs);
+}
+// Q4_1: d | m | qs[16]; d*q + m.  native.c:290-298
+template <>
+__device__ __forceinline__ float small_dot<T_Q4_1, 5>(const uint32_t (&w)[5], const float* x, float xs) {
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        lo[k] = oand(w[1 + k], 0x0F0F0F0Fu);
+        hi[k] = oand(w[1 + k], 0xF0F0F0F0u);
+    }
+    const float s = dot_run<4>(lo, x) + 0.0625f * dot_run<4>(hi, x + 16);
+    return half_bits_to_float(w[0]) * s + half_bits_to_float(w[0] >> 16) * xs;
+}
+// Q5_0: d | qh | qs[16]; d * (q5 - 16).  native.c:300-314
+template <>
+__device__ __forceinline__ float small_dot<T_Q5_0, 6>(const uint32_t (&w)[6], const float* x, float xs) {
+    const uint32_t qh = at_off(w, 0, 2);
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t v = at_off(w, k, 6);
+        lo[k] = oandor(v, 0x0F0F0F0Fu, spread4(qh >> (4 * k)) << 4);
+        hi[k] = oandor(v >> 4, 0x0F0F0F0Fu, spread4(qh >> (16 + 4 * k)) << 4);
+    }
+    const float s = dot_run<4>(lo, x) + dot_run<4>(hi, x + 16);
+    return half_bits_to_float(w[0]) * (s - 16.f * xs);
+}
+// Q5_1: d | m | qh | qs[16]; d*q5 + m.  native.c:316-328
+template <>
+__device__ __forceinline__ float small_dot<T_Q5_1, 6>(const uint32_t (&w)[6], const float* x, float xs) {
+    const uint32_t qh = w[1];
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t v = w[2 + k];
+        lo[k] = oandor(v, 0x0F0F0F0Fu, spread4(qh >> (4 * k)) << 4);
+        hi[k] = oandor(v >> 4, 0x0F0F0F0Fu, spread4(qh >> (16 + 4 * k)) << 4);
+    }
+    const float s = dot_run<4>(lo, x) + dot_run<4>(hi, x + 16);
+    return half_bits_to_float(w[0]) * s + half_bits_to_float(w[0] >> 16) * xs;
+}
+// Q8_0: d | i8 qs[32]; codes biased by +128 (xor 0x80) for unsigned conversion.  native.c:330-336
+template <>
+__device__ __forceinline__ float small_dot<T_Q8_0, 9>(const uint32_t (&w)[9], const float* x, float xs) {
+    uint32_t c[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) c[k] = at_off(w, k, 2) ^ 0x80808080u;
+    const float s = dot_run<8>(c, x);
+    return half_bits_to_float(w[0]) * (s - 128.f * xs);
+}
+// Q8_1: d | s | i8 qs[32].  native.c:338-344
+template <>
+__device__ __forceinline__ float small_dot<T_Q8_1, 9>(const uint32_t (&w)[9], const float* x, float xs) {
+    uint32_t c[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) c[k] = w[1 + k] ^ 0x80808080u;
+    const float s = dot_run<8>(c, x);
+    return half_bits_to_float(w[0]) * (s - 128.f * xs);
+}
+
+PYRITE_SMALL_UNIT(T_Q4_0)
+PYRITE_SMALL_UNIT(T_Q4_1)
+PYRITE_SMALL_UNIT(T_Q5_0)
+PYRITE_SMALL_UNIT(T_Q5_1)
+PYRITE_SMALL_UNIT(T_Q8_0)
+PYRITE_SMALL_UNIT(T_Q8_1)
+PYRITE_SMALL_UNIT(T_IQ4_NL)
+#undef PYRITE_SMALL_UNIT
+
+// ------------------------------------------------------------------ plain types
+// Four consecutive elements per unit (the last unit of a row may be partial).
+template <int T>
+__device__ __forceinline__ float plain_elem(const uint8_t* p) {
+    if constexpr (T == T_F32) return __uint_as_float(*reinterpret_cast<const uint32_t*>(p));
+    if constexpr (T == T_F16) return half_bits_to_float(*reinterpret_cast<const uint16_t*>(p));
+    if constexpr (T == T_BF16) return bf16_bits_to_float(*reinterpret_cast<const uint16_t*>(p));
+    if constexpr (T == T_I8) return (float)(int)*reinterpret_cast<const int8_t*>(p);
+    if constexpr (T == T_I16) return (float)(int)*reinterpret_cast<const int16_t*>(p);
+    if constexpr (T == T_I32) return (float)*reinterpret_cast<const int32_t*>(p);
+    if constexpr (T == T_I64) return (float)(double)*reinterpret_cast<const long long*>(p);
+    if constexpr (T == T_F64) return (float)*reinterpret_cast<const double*>(p);
+    return 0.f;
+}
+
+}  // namespace pyrite

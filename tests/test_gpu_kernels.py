@@ -1,0 +1,179 @@
+"""GPU parity of the dequant and dequant-matvec kernels against the oracle.
+
+Everything goes through the C ABI (include/pyrite_hip.h): the drop-in
+pyrite_matvec / pyrite_dequantize_rows via pyrite_amd.native, and the
+device-resident pyrite_dev_* entry points via pyrite_amd.device.
+
+Bars: dequantization is bit-exact (fp64 output == reference double; fp32 output
+== (float) of it); matvec is within 1e-4 * ||x||_2 * max|row| per row of the
+reference's fp64 result.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle.oracle import TYPES, oracle, row_bytes
+from tests.gpu_util import announce, assert_matvec_close, f32_bits_equal, f64_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+ALL_TYPES = sorted(TYPES)
+CASES = ["lcg", "rand", "special"]
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    from pyrite_amd import _lib
+
+    _lib.load()  # raises when the HIP library is missing: no silent fallback
+    return torch
+
+
+@pytest.fixture(scope="module")
+def golden(golden_dir):
+    return np.load(golden_dir / "native_kernels.npz")
+
+
+def _case(golden, t, case):
+    key = f"t{t}_{case}"
+    rows, cols = (int(v) for v in golden[key + "_shape"])
+    return key, rows, cols, golden[key + "_payload"], golden[key + "_x"]
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("t", ALL_TYPES, ids=lambda t: TYPES[t][0])
+def test_dropin_dequantize_is_bit_identical(torch_dev, golden, t, case):
+    from pyrite_amd import native
+
+    key, rows, cols, payload, _ = _case(golden, t, case)
+    announce("dropin_dequant", key, rows, cols)
+    got = np.array(native.dequantize_rows(t, payload.tobytes(), rows, cols))
+    ref = oracle().dequantize_rows(t, payload, rows, cols)
+    assert f64_bits_equal(got, ref)
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("t", ALL_TYPES, ids=lambda t: TYPES[t][0])
+def test_device_dequantize_f32_and_f64(torch_dev, golden, t, case):
+    torch = torch_dev
+    from pyrite_amd import device
+
+    key, rows, cols, payload, _ = _case(golden, t, case)
+    announce("device_dequant", key, rows, cols)
+    ref = oracle().dequantize_rows(t, payload, rows, cols)
+    w = device.upload(payload.tobytes())
+    d64 = device.dequantize(t, w, rows, cols, torch.float64).cpu().numpy().ravel()
+    d32 = device.dequantize(t, w, rows, cols, torch.float32).cpu().numpy().ravel()
+    assert f64_bits_equal(d64, ref)
+    assert f32_bits_equal(d32, ref.astype(np.float32))
+
+
+@pytest.mark.parametrize("case", CASES)
+@pytest.mark.parametrize("t", ALL_TYPES, ids=lambda t: TYPES[t][0])
+def test_dropin_matvec_matches_reference(torch_dev, golden, t, case):
+    from pyrite_amd import native
+
+    key, rows, cols, payload, x = _case(golden, t, case)
+    announce("dropin_matvec", key, rows, cols)
+    got = np.array(native.matvec(t, payload.tobytes(), list(x), rows, cols))
+    ref = golden[key + "_matvec"]
+    w = oracle().dequantize_rows(t, payload, rows, cols).reshape(rows, cols)
+    # fp64 on both sides, different summation order: bounded by n*eps*sum|w*x|
+    scale = np.nansum(np.abs(w) * np.abs(x)[None, :], axis=1)
+    finite = np.isfinite(ref)
+    assert np.all(np.abs(got[finite] - ref[finite]) <= 1e-12 * scale[finite]), key
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+
+
+def _weights(t, rows, cols, seed):
+    o = oracle()
+    if TYPES[t][1] == 1:  # plain types: random finite payloads
+        rng = np.random.default_rng(seed)
+        if t in (0, 28):
+            return rng.standard_normal(rows * cols).astype("<f4" if t == 0 else "<f8").view(np.uint8).copy()
+        if t == 1:
+            return (rng.standard_normal(rows * cols) * 3).astype("<f2").view(np.uint8).copy()
+        if t == 30:
+            v = rng.standard_normal(rows * cols).astype("<f4").view("<u4") >> 16
+            return v.astype("<u2").view(np.uint8).copy()
+        return rng.integers(0, 256, rows * row_bytes(t, cols), dtype=np.uint8)
+    return o.quantize(t, o.normal(seed, rows * cols, 0.0, 0.02).astype(np.float64))
+
+
+def _device_matvec_check(torch, t, rows, cols, batch, seed, offset=0):
+    from pyrite_amd import device
+
+    o = oracle()
+    payload = _weights(t, rows, cols, seed)
+    xs = np.stack([o.normal(seed + 1000 + b, cols) for b in range(batch)]).astype(np.float32)
+    buf = torch.zeros(payload.size + 16, dtype=torch.uint8, device="cuda")
+    buf[offset:offset + payload.size] = torch.from_numpy(payload).cuda()
+    w = buf[offset:offset + payload.size]
+    y = device.matvec(t, w, torch.from_numpy(xs).cuda(), rows, cols).cpu().numpy()
+    wd = o.dequantize_rows(t, payload, rows, cols).reshape(rows, cols)
+    rowmax = np.abs(wd).max(axis=1)
+    for b in range(batch):
+        ref = o.matvec(t, payload, xs[b].astype(np.float64), rows, cols)
+        assert_matvec_close(y[b], ref, xs[b], rowmax, f"{TYPES[t][0]} {rows}x{cols} b{b}/{batch} off{offset}")
+
+
+@pytest.mark.parametrize("batch", [1, 2, 3, 8, 11])
+@pytest.mark.parametrize("t", ALL_TYPES, ids=lambda t: TYPES[t][0])
+def test_device_matvec_batches(torch_dev, t, batch):
+    announce("device_matvec", TYPES[t][0], 37, 1024, batch)
+    _device_matvec_check(torch_dev, t, 37, 1024, batch, seed=7000 + t)
+
+
+@pytest.mark.parametrize("offset", [2, 4, 6])
+@pytest.mark.parametrize("t", ALL_TYPES, ids=lambda t: TYPES[t][0])
+def test_device_matvec_misaligned_weights(torch_dev, t, offset):
+    """Weights that start at any even offset (the verbatim GGUF contract is only
+    2-byte alignment per block); plain types need element alignment."""
+    from pyrite_amd import _lib
+
+    bpb = TYPES[t][2]
+    if TYPES[t][1] == 1 and offset % bpb:
+        with pytest.raises(_lib.KernelError) as err:
+            _device_matvec_check(torch_dev, t, 5, 256, 1, seed=11, offset=offset)
+        assert err.value.code == -3
+        return
+    announce("device_matvec_misaligned", TYPES[t][0], offset)
+    _device_matvec_check(torch_dev, t, 19, 768, 2, seed=8000 + t, offset=offset)
+
+
+@pytest.mark.parametrize("shape", [(1, 256), (5, 256), (64, 512), (129, 3072), (33, 14336)])
+@pytest.mark.parametrize("t", [2, 8, 12, 14, 11, 23, 0], ids=lambda t: TYPES[t][0])
+def test_device_matvec_edge_shapes(torch_dev, t, shape):
+    rows, cols = shape
+    announce("device_matvec_shape", TYPES[t][0], rows, cols)
+    _device_matvec_check(torch_dev, t, rows, cols, 1, seed=9000 + rows + t)
+
+
+# The type sweep over the Qwen3-0.6B decode projections at batch 1 and 8.
+SWEEP_TYPES = [2, 7, 8, 11, 13, 14, 23]  # Q4_0 Q5_1 Q8_0 Q3_K Q5_K Q6_K IQ4_XS
+PROJECTIONS = {"q": (2048, 1024), "k": (1024, 1024), "v": (1024, 1024), "o": (1024, 2048),
+               "gate": (3072, 1024), "up": (3072, 1024), "down": (1024, 3072)}
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+@pytest.mark.parametrize("t", SWEEP_TYPES, ids=lambda t: TYPES[t][0])
+def test_qwen3_projection_sweep(torch_dev, t, batch):
+    for i, (name, (rows, cols)) in enumerate(PROJECTIONS.items()):
+        announce("sweep", TYPES[t][0], name, rows, cols, batch)
+        _device_matvec_check(torch_dev, t, rows, cols, batch, seed=20242000 + 100 * t + i)
+
+
+def test_q4_k_config_one(torch_dev):
+    """Q4_K 3072 x 1024 from N(0, 0.02), x N(0, 1), batch 1."""
+    announce("config1 q4_k 3072x1024")
+    _device_matvec_check(torch_dev, 12, 3072, 1024, 1, seed=20241001)
+
+
+@pytest.mark.parametrize("t,rows,cols", [(12, 14336, 4096), (14, 4096, 14336), (12, 4096, 4096)])
+def test_llama_layer_shapes(torch_dev, t, rows, cols):
+    announce("llama", TYPES[t][0], rows, cols)
+    _device_matvec_check(torch_dev, t, rows, cols, 1, seed=20245000 + rows)
