@@ -67,6 +67,24 @@ int pyrite_dev_matvec(int type_id, const void *w, size_t w_len, size_t rows, siz
                       const float *x, size_t ldx, float *y, size_t ldy, size_t batch,
                       void *stream);
 
+/* One matrix of a grouped matvec: y[b * ldy + r] = sum_c dequant(w)[r][c] * x[b * ldx + c]. */
+typedef struct pyrite_matvec_desc {
+    const void *w;
+    size_t w_len;
+    size_t rows;
+    size_t cols;
+    const float *x;
+    size_t ldx;
+    float *y;
+    size_t ldy;
+} pyrite_matvec_desc;
+
+/* n same-type matrices (for example a layer's q/k/v, or gate/up) in one
+ * launch per 16 matrices; same rules as pyrite_dev_matvec for each.  Replaces
+ * the per-tensor loop of pyrite/executor.py:689-697 and 672-683. */
+int pyrite_dev_matvec_grouped(int type_id, const pyrite_matvec_desc *descs, size_t n,
+                              size_t batch, void *stream);
+
 /* Exact dequantization into device memory: fp32 when out_f64 == 0 (equal to
  * (float) of the reference double) or fp64 (bit-identical).  Replaces
  * pyrite_dequantize_rows at pyrite/executor.py:470-475 (embedding rows). */

@@ -48,6 +48,21 @@ inline TypeGeo type_geo(int id) {
     X(0) X(1) X(2) X(3) X(6) X(7) X(8) X(9) X(10) X(11) X(12) X(13) X(14) X(20) X(23) X(24) X(25) \
     X(26) X(27) X(28) X(30)
 
+// One matrix of a grouped matvec (same layout as pyrite_matvec_desc).
+struct MatvecArgs {
+    const void* w;
+    size_t w_len;
+    size_t rows;
+    size_t cols;
+    const float* x;
+    size_t ldx;
+    float* y;
+    size_t ldy;
+};
+
+// matvec.hip: several same-type matrices in one launch (16 per launch).
+int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, hipStream_t stream);
+
 // matvec.hip: Y[b][r] = sum_c W[r][c] X[b][c] in fp32, any batch (chunked by 8).
 // Returns 0, -1 (type), -2 (geometry), -3 (pointer/length/alignment), -4 (launch).
 int matvec_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* X, size_t ldx,

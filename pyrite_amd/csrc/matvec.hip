@@ -19,14 +19,35 @@
 
 namespace pyrite {
 
+// One matrix of a grouped launch.  wg_begin is the first workgroup (blockIdx.x)
+// assigned to this matrix; matrices occupy consecutive workgroup ranges.
+struct MvDesc {
+    const uint8_t* W;
+    unsigned long long row_bytes;
+    const float* X;
+    unsigned long long ldx;
+    float* Y;
+    unsigned long long ldy;
+    int rows;
+    int cols;
+    int lpr_log2;
+    int wg_begin;
+};
+
+constexpr int kMaxGroup = 16;
+struct MvGroup {
+    int n;
+    MvDesc d[kMaxGroup];
+};
+
 template <int T, int B, bool AL>
-__global__ __launch_bounds__(256) void mv_kernel(const uint8_t* __restrict__ W, unsigned long long row_bytes,
-                                                 int rows, int cols, const float* __restrict__ X,
-                                                 unsigned long long ldx, float* __restrict__ Y,
-                                                 unsigned long long ldy, int lpr_log2) {
+__device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* xs16) {
     constexpr int R = (B <= 2) ? 2 : 1;
     constexpr int BS = Geo<T>::bs, BPB = Geo<T>::bpb;
-    extern __shared__ float xs16[];
+    const uint8_t* __restrict__ W = d.W;
+    const float* __restrict__ X = d.X;
+    const int rows = d.rows, cols = d.cols, lpr_log2 = d.lpr_log2;
+    const unsigned long long ldx = d.ldx;
     const int n16 = cols >> 4;
     if constexpr (BS > 1) {
         for (int i = threadIdx.x; i < B * n16; i += blockDim.x) {
@@ -41,7 +62,7 @@ __global__ __launch_bounds__(256) void mv_kernel(const uint8_t* __restrict__ W, 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int LPR = 1 << lpr_log2, nslot = 64 >> lpr_log2;
     const int slot = lane >> lpr_log2, li = lane & (LPR - 1);
-    const long long wave_row0 = ((long long)blockIdx.x * 4 + wave) * nslot * R;
+    const long long wave_row0 = (wg * 4 + wave) * nslot * R;
     if (wave_row0 >= rows) return;
     const long long row0 = wave_row0 + (long long)slot * R;
 
@@ -55,7 +76,7 @@ __global__ __launch_bounds__(256) void mv_kernel(const uint8_t* __restrict__ W, 
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const long long rr = (row0 + r < rows) ? row0 + r : (long long)rows - 1;
-        rp[r] = W + rr * row_bytes;
+        rp[r] = W + rr * d.row_bytes;
     }
 
     if constexpr (BS > 1) {
@@ -102,95 +123,133 @@ __global__ __launch_bounds__(256) void mv_kernel(const uint8_t* __restrict__ W, 
         for (int r = 0; r < R; ++r)
             if (row0 + r < rows)
 #pragma unroll
-                for (int b = 0; b < B; ++b) Y[b * ldy + row0 + r] = acc[r][b];
+                for (int b = 0; b < B; ++b) d.Y[b * d.ldy + row0 + r] = acc[r][b];
     }
+}
+
+template <int T, int B, bool AL>
+__global__ __launch_bounds__(256) void mv_kernel(const MvGroup g) {
+    extern __shared__ float xs16[];
+    int i = 0;
+    while (i + 1 < g.n && (int)blockIdx.x >= g.d[i + 1].wg_begin) ++i;
+    mv_body<T, B, AL>(g.d[i], (long long)blockIdx.x - g.d[i].wg_begin, xs16);
 }
 
 // ---------------------------------------------------------------- launcher
 
-static int pow2_log2_ceil(long long v) {
+static int log2_ceil(long long v) {
     int l = 0;
     while ((1LL << l) < v) ++l;
     return l;
 }
 
-template <int T, int B, bool AL>
-static hipError_t launch_one(const uint8_t* W, size_t row_bytes, int rows, int cols, const float* X, size_t ldx,
-                             float* Y, size_t ldy, hipStream_t stream) {
+template <int T>
+static long long units_per_row(int cols) {
     constexpr int BS = Geo<T>::bs;
-    long long U;
-    if constexpr (BS > 1) U = (long long)(cols / BS) * Unit<T>::P;
-    else U = (cols + 3) / 4;
-    const int lpr_log2 = pow2_log2_ceil(U < 64 ? U : 64);
-    const int nslot = 64 >> lpr_log2;
+    if constexpr (BS > 1) return (long long)(cols / BS) * Unit<T>::P;
+    else return (cols + 3) / 4;
+}
+
+// Fill lpr_log2 / wg_begin for B and return the total number of workgroups.
+template <int T, int B>
+static long long plan_group(MvGroup& g) {
     const int R = (B <= 2) ? 2 : 1;
-    const long long rows_per_wg = 4LL * nslot * R;
-    const long long grid = (rows + rows_per_wg - 1) / rows_per_wg;
-    const size_t lds = (BS > 1) ? (size_t)B * (cols / 16) * sizeof(float) : 0;
-    hipLaunchKernelGGL((mv_kernel<T, B, AL>), dim3((unsigned)grid), dim3(256), lds, stream, W,
-                       (unsigned long long)row_bytes, rows, cols, X, (unsigned long long)ldx, Y,
-                       (unsigned long long)ldy, lpr_log2);
+    long long wg = 0;
+    for (int i = 0; i < g.n; ++i) {
+        const long long U = units_per_row<T>(g.d[i].cols);
+        g.d[i].lpr_log2 = log2_ceil(U < 64 ? U : 64);
+        const long long rows_per_wg = 4LL * (64 >> g.d[i].lpr_log2) * R;
+        g.d[i].wg_begin = (int)wg;
+        wg += (g.d[i].rows + rows_per_wg - 1) / rows_per_wg;
+    }
+    return wg;
+}
+
+template <int T, int B, bool AL>
+static hipError_t launch_group(MvGroup g, size_t lds, hipStream_t stream) {
+    const long long wgs = plan_group<T, B>(g);
+    if (wgs <= 0 || wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((mv_kernel<T, B, AL>), dim3((unsigned)wgs), dim3(256), lds, stream, g);
     return hipGetLastError();
 }
 
 template <int T, bool AL>
-static hipError_t launch_type(int batch, const uint8_t* W, size_t row_bytes, int rows, int cols, const float* X,
-                              size_t ldx, float* Y, size_t ldy, hipStream_t s) {
+static hipError_t launch_type(int batch, const MvGroup& g, size_t lds, hipStream_t s) {
     switch (batch) {
-    case 1: return launch_one<T, 1, AL>(W, row_bytes, rows, cols, X, ldx, Y, ldy, s);
-    case 2: return launch_one<T, 2, AL>(W, row_bytes, rows, cols, X, ldx, Y, ldy, s);
-    case 4: return launch_one<T, 4, AL>(W, row_bytes, rows, cols, X, ldx, Y, ldy, s);
-    case 8: return launch_one<T, 8, AL>(W, row_bytes, rows, cols, X, ldx, Y, ldy, s);
+    case 1: return launch_group<T, 1, AL>(g, lds, s);
+    case 2: return launch_group<T, 2, AL>(g, lds, s);
+    case 4: return launch_group<T, 4, AL>(g, lds, s);
+    case 8: return launch_group<T, 8, AL>(g, lds, s);
     default: return hipErrorInvalidValue;
     }
 }
 
-// Largest batch chunk the kernels are instantiated for that fits `left` and the
-// LDS budget for the per-16-column sums (64 KiB).
-static int pick_chunk(int left, int cols, bool quant) {
-    const int cand[4] = {8, 4, 2, 1};
-    for (int c : cand) {
-        if (c > left) continue;
-        if (!quant || (size_t)c * (cols / 16) * sizeof(float) <= 65536) return c;
+int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, hipStream_t stream) {
+    const TypeGeo g = type_geo(type);
+    if (!g.valid) return -1;
+    if (n == 0 || batch == 0) return -2;
+    const bool quant = g.bs > 1;
+    bool al = (g.bpb % 4 == 0);
+    size_t max_cols = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const MatvecArgs& m = mats[i];
+        if (m.rows == 0 || m.cols == 0 || m.cols % g.bs != 0) return -2;
+        if (m.rows > 0x7FFFFFFF || m.cols > 0x7FFFFFFF) return -2;
+        const size_t row_bytes = m.cols / g.bs * g.bpb;
+        if (m.w_len != m.rows * row_bytes) return -3;
+        if (!m.w || !m.x || !m.y || m.ldx < m.cols || m.ldy < m.rows) return -3;
+        if (quant && ((reinterpret_cast<uintptr_t>(m.x) & 15u) || (m.ldx & 3u))) return -3;
+        if (!quant && (reinterpret_cast<uintptr_t>(m.w) % g.bpb)) return -3;
+        if (reinterpret_cast<uintptr_t>(m.w) & 3u) al = false;
+        if (m.cols > max_cols) max_cols = m.cols;
+    }
+    size_t done = 0;
+    while (done < batch) {
+        // largest instantiated batch chunk whose per-16-column x sums fit 64 KiB of LDS
+        int c = 0;
+        for (int cand : {8, 4, 2, 1}) {
+            if ((size_t)cand > batch - done) continue;
+            if (!quant || (size_t)cand * (max_cols / 16) * sizeof(float) <= 65536) { c = cand; break; }
+        }
+        if (c == 0) return -2;
+        const size_t lds = quant ? (size_t)c * (max_cols / 16) * sizeof(float) : 0;
+        for (size_t base = 0; base < n; base += kMaxGroup) {
+            MvGroup grp;
+            grp.n = (int)((n - base) < (size_t)kMaxGroup ? (n - base) : (size_t)kMaxGroup);
+            for (int i = 0; i < grp.n; ++i) {
+                const MatvecArgs& m = mats[base + i];
+                MvDesc& dd = grp.d[i];
+                dd.W = static_cast<const uint8_t*>(m.w);
+                dd.row_bytes = m.cols / g.bs * g.bpb;
+                dd.X = m.x + done * m.ldx;
+                dd.ldx = m.ldx;
+                dd.Y = m.y + done * m.ldy;
+                dd.ldy = m.ldy;
+                dd.rows = (int)m.rows;
+                dd.cols = (int)m.cols;
+            }
+            hipError_t e = hipSuccess;
+#define PYRITE_CASE(T)                                                                       \
+    case T:                                                                                \
+        e = al ? launch_type<T, (Geo<T>::bpb % 4 == 0)>(c, grp, lds, stream)               \
+               : launch_type<T, false>(c, grp, lds, stream);                               \
+        break;
+            switch (type) {
+                PYRITE_FOR_EACH_TYPE(PYRITE_CASE)
+            default: return -1;
+            }
+#undef PYRITE_CASE
+            if (e != hipSuccess) return -4;
+        }
+        done += c;
     }
     return 0;
 }
 
 int matvec_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* X, size_t ldx,
                   float* Y, size_t ldy, size_t batch, hipStream_t stream) {
-    const TypeGeo g = type_geo(type);
-    if (!g.valid) return -1;
-    if (rows == 0 || cols == 0 || batch == 0 || cols % g.bs != 0) return -2;
-    if (rows > 0x7FFFFFFF || cols > 0x7FFFFFFF) return -2;
-    const size_t row_bytes = cols / g.bs * g.bpb;
-    if (w_len != rows * row_bytes) return -3;
-    if (!W || !X || !Y || ldx < cols || ldy < rows) return -3;
-    const bool quant = g.bs > 1;
-    if (quant && ((reinterpret_cast<uintptr_t>(X) & 15u) || (ldx & 3u))) return -3;
-    if (!quant && (reinterpret_cast<uintptr_t>(W) % g.bpb)) return -3;
-    const bool al = (g.bpb % 4 == 0) && ((reinterpret_cast<uintptr_t>(W) & 3u) == 0);
-    size_t done = 0;
-    while (done < batch) {
-        const int c = pick_chunk((int)(batch - done > 8 ? 8 : batch - done), (int)cols, quant);
-        if (c == 0) return -2;
-        hipError_t e = hipSuccess;
-        const float* Xc = X + done * ldx;
-        float* Yc = Y + done * ldy;
-#define PYRITE_CASE(T)                                                                                  \
-    case T:                                                                                           \
-        e = (al && Geo<T>::bpb % 4 == 0)                                                              \
-                ? launch_type<T, (Geo<T>::bpb % 4 == 0)>(c, W, row_bytes, (int)rows, (int)cols, Xc, ldx, Yc, ldy, stream) \
-                : launch_type<T, false>(c, W, row_bytes, (int)rows, (int)cols, Xc, ldx, Yc, ldy, stream);  \
-        break;
-        switch (type) {
-            PYRITE_FOR_EACH_TYPE(PYRITE_CASE)
-        default: return -1;
-        }
-#undef PYRITE_CASE
-        if (e != hipSuccess) return -4;
-        done += c;
-    }
-    return 0;
+    MatvecArgs m{W, w_len, rows, cols, X, ldx, Y, ldy};
+    return matvec_group_launch(type, &m, 1, batch, stream);
 }
 
 }  // namespace pyrite

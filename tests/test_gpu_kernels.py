@@ -177,3 +177,44 @@ def test_q4_k_config_one(torch_dev):
 def test_llama_layer_shapes(torch_dev, t, rows, cols):
     announce("llama", TYPES[t][0], rows, cols)
     _device_matvec_check(torch_dev, t, rows, cols, 1, seed=20245000 + rows)
+
+
+@pytest.mark.parametrize("batch", [1, 8])
+@pytest.mark.parametrize("t", [2, 12, 14, 23, 0], ids=lambda t: TYPES[t][0])
+def test_grouped_matvec_equals_single_launches(torch_dev, t, batch):
+    """pyrite_dev_matvec_grouped over mixed shapes gives, bit for bit, what one
+    pyrite_dev_matvec per matrix gives, and both meet the oracle bar."""
+    import ctypes
+
+    torch = torch_dev
+    from pyrite_amd import _lib, device
+
+    o = oracle()
+    lib = _lib.load()
+    shapes = [(2048, 1024), (1024, 1024), (1024, 2048), (333, 3072), (7, 256)]
+    mats = []
+    for i, (rows, cols) in enumerate(shapes):
+        payload = _weights(t, rows, cols, 31000 + i)
+        x = np.stack([o.normal(32000 + 10 * i + b, cols) for b in range(batch)]).astype(np.float32)
+        mats.append((rows, cols, payload, torch.from_numpy(payload).cuda(), torch.from_numpy(x).cuda(), x))
+    announce("grouped", TYPES[t][0], batch, len(shapes))
+
+    class Desc(ctypes.Structure):
+        _fields_ = [("w", ctypes.c_void_p), ("w_len", ctypes.c_size_t), ("rows", ctypes.c_size_t),
+                    ("cols", ctypes.c_size_t), ("x", ctypes.c_void_p), ("ldx", ctypes.c_size_t),
+                    ("y", ctypes.c_void_p), ("ldy", ctypes.c_size_t)]
+
+    ys = [torch.full((batch, rows), float("nan"), device="cuda") for rows, *_ in mats]
+    arr = (Desc * len(mats))()
+    for i, (rows, cols, payload, w, xg, _) in enumerate(mats):
+        arr[i] = Desc(w.data_ptr(), payload.nbytes, rows, cols, xg.data_ptr(), cols, ys[i].data_ptr(), rows)
+    stream = torch.cuda.current_stream().cuda_stream
+    _lib.check(lib.pyrite_dev_matvec_grouped(t, arr, len(mats), batch, ctypes.c_void_p(stream)), "grouped")
+    for i, (rows, cols, payload, w, xg, x) in enumerate(mats):
+        single = device.matvec(t, w, xg, rows, cols)
+        assert torch.equal(single, ys[i]), f"matrix {i}"
+        rowmax = np.abs(o.dequantize_rows(t, payload, rows, cols).reshape(rows, cols)).max(axis=1)
+        got = ys[i].cpu().numpy()
+        for b in range(batch):
+            ref = o.matvec(t, payload, x[b].astype(np.float64), rows, cols)
+            assert_matvec_close(got[b], ref, x[b], rowmax, f"grouped {i} b{b}")
