@@ -12,8 +12,10 @@ One step = for batch in (1, 8), for each type: one grouped launch
 are uploaded verbatim and rotated over 4 device copies (305 MB > the 256 MB
 Infinity Cache), so every launch reads its weights from HBM.  The timed steps
 are captured into one HIP graph and replayed once between two
-synchronisations; timing events recorded inside the graph around every launch
-give each kernel's duration for the roofline.
+synchronisations.  Each kernel's duration for the roofline comes from HIP
+events that the launch itself records at kernel start and end
+(hipExtLaunchKernelGGL), over the same launches replayed eagerly on the same
+stream right after the timed replay.
 
 Prints one JSON line.  value = quantized weight bytes / second over the timed
 steps (GB/s).  --gpus N > 1 exits: this path runs on one GPU.
@@ -155,7 +157,11 @@ def main() -> int:
                     arr[i] = Desc(copies[c].data_ptr(), payload.nbytes, rows, cols, x.data_ptr(), cols,
                                   y.data_ptr(), rows)
                 descs[(t, b, c)] = arr
-    stream = torch.cuda.current_stream()
+    # all work goes on one side stream (default priority): graphs cannot be
+    # captured on the default stream
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    torch.cuda.set_stream(stream)
     sptr = ctypes.c_void_p(stream.cuda_stream)
     fn = lib.pyrite_dev_matvec_grouped
 
@@ -179,25 +185,11 @@ def main() -> int:
     torch.cuda.synchronize()
     eager_out = {k: v.clone() for k, v in ys.items()}
 
-    def new_events():
-        return [[torch.cuda.Event(enable_timing=True, external=True) for _ in range(2)] for _ in launches]
-
-    ev = [new_events() for _ in range(args.steps)]
-    graph_events = True
     g = torch.cuda.CUDAGraph()
-    try:
-        with torch.cuda.graph(g, stream=stream):
-            for s in range(args.steps):
-                step(s, ev[s])
-    except Exception as exc:  # timing events inside a graph unsupported: capture without them
-        log(f"graph capture with timing events failed ({exc!r}); capturing without")
-        graph_events = False
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            for s in range(args.steps):
-                step(s)
-    stream = torch.cuda.current_stream()
-    g.replay()  # graph warm-up
+    with torch.cuda.graph(g, stream=stream):
+        for s in range(args.steps):
+            step(s)
+    g.replay()  # graph warm-up, checked against the eager launches
     torch.cuda.synchronize()
     for k, v in ys.items():
         if not torch.equal(v, eager_out[k]):
@@ -211,30 +203,29 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     value = bytes_per_step * args.steps / elapsed / 1e9
 
-    # per-kernel durations from the events recorded inside the replayed graph
+    # Per-kernel durations: the same launches again, eagerly, each timed by HIP
+    # events that the launch itself records at kernel start and end
+    # (pyrite_dev_matvec_grouped_timed -> hipExtLaunchKernelGGL), on this stream.
+    log("per-kernel timing pass")
+    timed = lib.pyrite_dev_matvec_grouped_timed
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in launches]
+    for pair in evs:
+        for e in pair:
+            e.record(stream)  # creates the underlying hipEvent_t
+    torch.cuda.synchronize()
     durations = {}
-    if graph_events:
-        try:
-            for s in range(args.steps):
-                for k, key in enumerate(launches):
-                    durations.setdefault(key, []).append(ev[s][k][0].elapsed_time(ev[s][k][1]) * 1e-3)
-        except Exception as exc:
-            log(f"reading graph timing events failed ({exc!r})")
-            durations = {}
-    timing_source = "events inside the timed graph replay"
-    if not durations:
-        timing_source = "events around eager launches right after the timed region"
-        evs = new_events()
-        for s in range(args.steps):
-            for k, key in enumerate(launches):
-                t, b = key
-                c = (2 * s + BATCHES.index(b)) % COPIES
-                evs[k][0].record(stream)
-                fn(t, descs[(t, b, c)], len(PROJECTIONS), b, sptr)
-                evs[k][1].record(stream)
-            torch.cuda.synchronize()
-            for k, key in enumerate(launches):
-                durations.setdefault(key, []).append(evs[k][0].elapsed_time(evs[k][1]) * 1e-3)
+    for s in range(args.steps):
+        for k, (t, b) in enumerate(launches):
+            c = (2 * s + BATCHES.index(b)) % COPIES
+            rc = timed(t, descs[(t, b, c)], len(PROJECTIONS), b, sptr, ctypes.c_void_p(evs[k][0].cuda_event),
+                       ctypes.c_void_p(evs[k][1].cuda_event))
+            if rc != 0:
+                raise RuntimeError(f"timed launch failed: {rc} {_lib.last_error()}")
+        torch.cuda.synchronize()
+        for k, key in enumerate(launches):
+            durations.setdefault(key, []).append(evs[k][0].elapsed_time(evs[k][1]) * 1e-3)
+    timing_source = ("HIP events recorded by each launch at kernel start/end (hipExtLaunchKernelGGL), "
+                     "same launches and weight rotation as the timed graph, on the same stream")
 
     per_kernel = {}
     for (t, b), ds in durations.items():

@@ -85,6 +85,13 @@ typedef struct pyrite_matvec_desc {
 int pyrite_dev_matvec_grouped(int type_id, const pyrite_matvec_desc *descs, size_t n,
                               size_t batch, void *stream);
 
+/* As pyrite_dev_matvec_grouped, with HIP events (hipEvent_t, may be NULL)
+ * recorded by the first launch at its start and by the last at its end, so
+ * they time the kernels themselves rather than host submission. */
+int pyrite_dev_matvec_grouped_timed(int type_id, const pyrite_matvec_desc *descs, size_t n,
+                                    size_t batch, void *stream, void *start_event,
+                                    void *stop_event);
+
 /* Exact dequantization into device memory: fp32 when out_f64 == 0 (equal to
  * (float) of the reference double) or fp64 (bit-identical).  Replaces
  * pyrite_dequantize_rows at pyrite/executor.py:470-475 (embedding rows). */

@@ -23,6 +23,8 @@ SIGNATURES: list[tuple[str, object, tuple]] = [
     ("pyrite_dequantize_rows", _c.c_int, (_c.c_int, _vp, _sz, _dp, _sz, _sz)),
     ("pyrite_hip_last_error", _c.c_char_p, ()),
     ("pyrite_dev_matvec", _c.c_int, (_c.c_int, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _sz, _vp)),
+    ("pyrite_dev_matvec_grouped", _c.c_int, (_c.c_int, _vp, _sz, _sz, _vp)),
+    ("pyrite_dev_matvec_grouped_timed", _c.c_int, (_c.c_int, _vp, _sz, _sz, _vp, _vp, _vp)),
     ("pyrite_dev_dequantize", _c.c_int, (_c.c_int, _vp, _sz, _sz, _sz, _vp, _c.c_int, _vp)),
 ]
 

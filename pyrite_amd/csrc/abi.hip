@@ -155,6 +155,16 @@ int pyrite_dev_matvec_grouped(int type_id, const pyrite_matvec_desc* descs, size
     return rc;
 }
 
+int pyrite_dev_matvec_grouped_timed(int type_id, const pyrite_matvec_desc* descs, size_t n, size_t batch,
+                                    void* stream, void* start_event, void* stop_event) {
+    if (descs == NULL) return -3;
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;
+    const int rc = matvec_group_launch(type_id, reinterpret_cast<const MatvecArgs*>(descs), n, batch, s,
+                                       static_cast<hipEvent_t>(start_event), static_cast<hipEvent_t>(stop_event));
+    if (rc == -4) return fail(-4, "pyrite_dev_matvec_grouped_timed: launch", hipGetLastError());
+    return rc;
+}
+
 int pyrite_dev_dequantize(int type_id, const void* w, size_t w_len, size_t rows, size_t cols, void* out,
                           int out_f64, void* stream) {
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;

@@ -61,7 +61,15 @@ struct MatvecArgs {
 };
 
 // matvec.hip: several same-type matrices in one launch (16 per launch).
-int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, hipStream_t stream);
+// start/stop (optional) are recorded by the first / last launch itself.
+int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, hipStream_t stream,
+                        hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
+
+// mx.hip: MFMA path for the quantized block formats, up to 8 vectors starting
+// at vector `done` of each matrix (arguments already validated).
+bool mx_type_supported(int type);
+int mx_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, size_t done, bool al,
+                    hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
 // matvec.hip: Y[b][r] = sum_c W[r][c] X[b][c] in fp32, any batch (chunked by 8).
 // Returns 0, -1 (type), -2 (geometry), -3 (pointer/length/alignment), -4 (launch).

@@ -11,20 +11,46 @@
 // unit follows each block layout (pyrite/kernels/native.c:129-437).
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace pyrite {
 
+typedef __attribute__((address_space(3))) float lds_f;
+
+typedef float f4n __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) f4n lds_f4;
+
+__device__ __forceinline__ float4 ld_x4(const lds_f* p) {
+    const f4n v = *(const lds_f4*)(p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void st_x4(lds_f* p, float4 v) {
+    *(lds_f4*)(p) = f4n{v.x, v.y, v.z, v.w};
+}
+
+// Activations seen by one unit.  With XL the activations are staged in LDS
+// with 4 floats of padding after every PADI floats (PADI = the unit stride of
+// the format, so consecutive lanes read distinct bank groups); ptr(b, off)
+// maps a column offset inside the current block to the (padded) address.
+// Block starts are multiples of PADI, so padding is additive across them.
+template <bool XL, int PADI>
 struct XView {
-    const float* x;     // activations of column 0 of this block, batch 0
+    using P = typename std::conditional<XL, const lds_f*, const float*>::type;
+    P x;                // activations of column 0 of this block, batch 0
     size_t ldx;         // floats between batch rows
-    const float* xs16;  // LDS: sum of each 16 columns, batch 0, from column 0 of this block
+    const lds_f* xs16;  // LDS: sum of each 16 columns, batch 0, from column 0 of this block
     int ld16;           // floats between batch rows in xs16
+    __device__ __forceinline__ P ptr(int b, int off) const {
+        if constexpr (XL) return x + b * ldx + off + (off / PADI) * 4;
+        else return x + b * ldx + off;
+    }
 };
 
-// sum over 16 consecutive columns of u32 codes (4 per dword) against x
-template <int NW>
-__device__ __forceinline__ float dot_run(const uint32_t (&c)[NW], const float* x) {
+// sum over 4*NW consecutive columns of u32 codes (4 per dword) against x
+template <int NW, typename PX>
+__device__ __forceinline__ float dot_run(const uint32_t (&c)[NW], PX x) {
     float s = 0.f;
 #pragma unroll
     for (int k = 0; k < NW; ++k) s = dot_ub4(c[k], ld_x4(x + 4 * k), s);
@@ -55,9 +81,9 @@ __device__ __forceinline__ void k4_pair_regs(uint32_t s0, uint32_t s1, uint32_t 
 }
 
 template <> struct Unit<T_Q4_K> {
-    static constexpr int P = 4;
-    template <int B, int R, bool AL>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int c, const XView& xv,
+    static constexpr int P = 4, PADI = 64;
+    template <int B, int R, bool AL, class XV>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int c, const XV& xv,
                                                float (&acc)[R][B]) {
         uint32_t hd[R][4], q[R][8];
 #pragma unroll
@@ -67,8 +93,8 @@ template <> struct Unit<T_Q4_K> {
         }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const float* x = xv.x + b * xv.ldx + 64 * c;
-            const float* s16 = xv.xs16 + b * xv.ld16 + 4 * c;
+            const auto x = xv.ptr(b, 64 * c), xh = xv.ptr(b, 64 * c + 32);
+            const lds_f* s16 = xv.xs16 + b * xv.ld16 + 4 * c;
             const float xlo = s16[0] + s16[1], xhi = s16[2] + s16[3];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -76,7 +102,7 @@ template <> struct Unit<T_Q4_K> {
 #pragma unroll
                 for (int k = 0; k < 8; ++k) { lo[k] = oand(q[r][k], 0x0F0F0F0Fu); hi[k] = oand(q[r][k], 0xF0F0F0F0u); }
                 const float slo = dot_run<8>(lo, x);
-                const float shi = dot_run<8>(hi, x + 32);
+                const float shi = dot_run<8>(hi, xh);
                 float sc0, m0, sc1, m1;
                 k4_pair_regs(hd[r][1], hd[r][2], hd[r][3], c, sc0, m0, sc1, m1);
                 const float d = half_bits_to_float(hd[r][0]), dmin = half_bits_to_float(hd[r][0] >> 16);
@@ -89,9 +115,9 @@ template <> struct Unit<T_Q4_K> {
 // ------------------------------------------------------------------ Q5_K
 // as Q4_K plus a fifth bit: qh[l] bit 2c (low) / 2c+1 (high).  native.c:410-437
 template <> struct Unit<T_Q5_K> {
-    static constexpr int P = 4;
-    template <int B, int R, bool AL>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int c, const XView& xv,
+    static constexpr int P = 4, PADI = 64;
+    template <int B, int R, bool AL, class XV>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int c, const XV& xv,
                                                float (&acc)[R][B]) {
         uint32_t hd[R][4], q[R][8], h[R][8];
 #pragma unroll
@@ -102,8 +128,8 @@ template <> struct Unit<T_Q5_K> {
         }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const float* x = xv.x + b * xv.ldx + 64 * c;
-            const float* s16 = xv.xs16 + b * xv.ld16 + 4 * c;
+            const auto x = xv.ptr(b, 64 * c), xh = xv.ptr(b, 64 * c + 32);
+            const lds_f* s16 = xv.xs16 + b * xv.ld16 + 4 * c;
             const float xlo = s16[0] + s16[1], xhi = s16[2] + s16[3];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
@@ -114,7 +140,7 @@ template <> struct Unit<T_Q5_K> {
                     hi[k] = oandor(q[r][k] >> 4, 0x0F0F0F0Fu, ((h[r][k] >> (2 * c + 1)) & 0x01010101u) << 4);
                 }
                 const float slo = dot_run<8>(lo, x);
-                const float shi = dot_run<8>(hi, x + 32);
+                const float shi = dot_run<8>(hi, xh);
                 float sc0, m0, sc1, m1;
                 k4_pair_regs(hd[r][1], hd[r][2], hd[r][3], c, sc0, m0, sc1, m1);
                 const float d = half_bits_to_float(hd[r][0]), dmin = half_bits_to_float(hd[r][0] >> 16);
@@ -129,9 +155,9 @@ template <> struct Unit<T_Q5_K> {
 // l = 0..15.  ql bytes 64h+16r'+l (g even) and 64h+32+16r'+l (g odd), nibble
 // g >> 1; qh byte 32h+16r'+l bits 2g; scale 8h + 2g + r'.  native.c:199-225
 template <> struct Unit<T_Q6_K> {
-    static constexpr int P = 4;
-    template <int B, int R, bool AL>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XView& xv,
+    static constexpr int P = 4, PADI = 128;
+    template <int B, int R, bool AL, class XV>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XV& xv,
                                                float (&acc)[R][B]) {
         const int h = u >> 1, rr = u & 1;
         uint32_t A[R][4], Bq[R][4], H[R][4], S[R][2], D[R][1];
@@ -145,8 +171,8 @@ template <> struct Unit<T_Q6_K> {
         }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const float* x = xv.x + b * xv.ldx + 128 * h + 16 * rr;
-            const float* s16 = xv.xs16 + b * xv.ld16 + 8 * h + rr;
+            const int xo = 128 * h + 16 * rr;
+            const lds_f* s16 = xv.xs16 + b * xv.ld16 + 8 * h + rr;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 float tot = 0.f;
@@ -159,7 +185,7 @@ template <> struct Unit<T_Q6_K> {
                         c[k] = oandor((g & 2) ? (lq >> 4) : lq, 0x0F0F0F0Fu,
                                       ((H[r][k] >> (2 * g)) & 0x03030303u) << 4);
                     }
-                    const float sg = dot_run<4>(c, x + 32 * g);
+                    const float sg = dot_run<4>(c, xv.ptr(b, xo + 32 * g));
                     const uint32_t sw = S[r][g >> 1] >> (8 * (rr + 2 * (g & 1)));
                     const float sc = (float)(int)(int8_t)(sw & 0xFF);
                     tot += sc * (sg - 32.f * s16[2 * g]);
@@ -175,9 +201,9 @@ template <> struct Unit<T_Q6_K> {
 // 128h + 32g + 16r' + l at bits 2g; scale byte 8h + 2g + r' (low nibble scale,
 // high nibble min); d, dmin at 80, 82.  native.c:381-408
 template <> struct Unit<T_Q2_K> {
-    static constexpr int P = 4;
-    template <int B, int R, bool AL>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XView& xv,
+    static constexpr int P = 4, PADI = 128;
+    template <int B, int R, bool AL, class XV>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XV& xv,
                                                float (&acc)[R][B]) {
         const int h = u >> 1, rr = u & 1;
         uint32_t Q[R][4], S[R][2], D[R][1];
@@ -189,8 +215,8 @@ template <> struct Unit<T_Q2_K> {
         }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const float* x = xv.x + b * xv.ldx + 128 * h + 16 * rr;
-            const float* s16 = xv.xs16 + b * xv.ld16 + 8 * h + rr;
+            const int xo = 128 * h + 16 * rr;
+            const lds_f* s16 = xv.xs16 + b * xv.ld16 + 8 * h + rr;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 float ts = 0.f, tm = 0.f;
@@ -199,7 +225,7 @@ template <> struct Unit<T_Q2_K> {
                     uint32_t c[4];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) c[k] = oand(Q[r][k] >> (2 * g), 0x03030303u);
-                    const float sg = dot_run<4>(c, x + 32 * g);
+                    const float sg = dot_run<4>(c, xv.ptr(b, xo + 32 * g));
                     const uint32_t sb = (S[r][g >> 1] >> (8 * (rr + 2 * (g & 1)))) & 0xFF;
                     ts += (float)(sb & 15) * sg;
                     tm += (float)(sb >> 4) * s16[2 * g];
@@ -215,9 +241,9 @@ template <> struct Unit<T_Q2_K> {
 // byte 16r'+l bit 4h+g (clear = subtract 4), 6-bit scale j = 8h+2g+r' from the
 // 12 packed bytes at 96, d at 108.  native.c:129-171
 template <> struct Unit<T_Q3_K> {
-    static constexpr int P = 4;
-    template <int B, int R, bool AL>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XView& xv,
+    static constexpr int P = 4, PADI = 128;
+    template <int B, int R, bool AL, class XV>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XV& xv,
                                                float (&acc)[R][B]) {
         const int h = u >> 1, rr = u & 1;
         uint32_t Q[R][4], M[R][4], S[R][3], D[R][1];
@@ -230,8 +256,8 @@ template <> struct Unit<T_Q3_K> {
         }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const float* x = xv.x + b * xv.ldx + 128 * h + 16 * rr;
-            const float* s16 = xv.xs16 + b * xv.ld16 + 8 * h + rr;
+            const int xo = 128 * h + 16 * rr;
+            const lds_f* s16 = xv.xs16 + b * xv.ld16 + 8 * h + rr;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 float tot = 0.f;
@@ -242,7 +268,7 @@ template <> struct Unit<T_Q3_K> {
                     for (int k = 0; k < 4; ++k)
                         c[k] = oandor(Q[r][k] >> (2 * g), 0x03030303u,
                                       ((M[r][k] >> (4 * h + g)) & 0x01010101u) << 2);
-                    const float sg = dot_run<4>(c, x + 32 * g);
+                    const float sg = dot_run<4>(c, xv.ptr(b, xo + 32 * g));
                     // j = 8h + 2g + r': low nibble from byte 2g + r' (h selects the nibble),
                     // top two bits from byte 8 + (2g + r') % 4 at bit 2 * (2h + g / 2)
                     const uint32_t lb = (S[r][g >> 1] >> (8 * (rr + 2 * (g & 1)))) & 0xFF;
@@ -263,9 +289,9 @@ template <> struct Unit<T_Q3_K> {
 // high -> 32ib + 16 + j; 6-bit scale ls from scales_l / scales_h, value
 // d*(ls-32)*K[n].  native.c:364-379
 template <> struct Unit<T_IQ4_XS> {
-    static constexpr int P = 4;
-    template <int B, int R, bool AL>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XView& xv,
+    static constexpr int P = 4, PADI = 64;
+    template <int B, int R, bool AL, class XV>
+    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XV& xv,
                                                float (&acc)[R][B]) {
         uint32_t hd[R][2], q[R][8];
 #pragma unroll
@@ -275,8 +301,7 @@ template <> struct Unit<T_IQ4_XS> {
         }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const float* x = xv.x + b * xv.ldx + 64 * u;
-            const float* s16 = xv.xs16 + b * xv.ld16 + 4 * u;
+            const lds_f* s16 = xv.xs16 + b * xv.ld16 + 4 * u;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const uint32_t sl = (hd[r][1] >> (8 * u)) & 0xFF;
@@ -292,7 +317,7 @@ template <> struct Unit<T_IQ4_XS> {
                         lo[k] = iq4_lut4(q[r][4 * s + k] & 0x0F0F0F0Fu);
                         hi[k] = iq4_lut4((q[r][4 * s + k] >> 4) & 0x0F0F0F0Fu);
                     }
-                    const float sv = dot_run<4>(lo, x + 32 * s) + dot_run<4>(hi, x + 32 * s + 16);
+                    const float sv = dot_run<4>(lo, xv.ptr(b, 64 * u + 32 * s)) + dot_run<4>(hi, xv.ptr(b, 64 * u + 32 * s + 16));
                     const float xs = s16[2 * s] + s16[2 * s + 1];
                     tot += ((float)(int)ls - 32.f) * (sv - 128.f * xs);
                 }
@@ -322,28 +347,27 @@ __device__ __forceinline__ uint32_t at_off(const uint32_t (&w)[N], int k, int of
 
 #define PYRITE_SMALL_UNIT(T)                                                                         \
     template <> struct Unit<T> {                                                                     \
-        static constexpr int P = 1;                                                                  \
+        static constexpr int P = 1, PADI = 32;                                                       \
         static constexpr int NB = Small<T>::NB;                                                      \
-        template <int B, int R, bool AL>                                                             \
-        __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int, const XView& xv, \
+        template <int B, int R, bool AL, class XV>                                                   \
+        __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int, const XV& xv,  \
                                                    float (&acc)[R][B]) {                             \
             uint32_t w[R][(NB + 3) / 4];                                                             \
             _Pragma("unroll") for (int r = 0; r < R; ++r) ld_span<NB, AL>(blk[r], w[r]);              \
             _Pragma("unroll") for (int b = 0; b < B; ++b) {                                          \
-                const float* x = xv.x + b * xv.ldx;                                                  \
-                const float* s16 = xv.xs16 + b * xv.ld16;                                            \
+                const auto x0 = xv.ptr(b, 0), x16 = xv.ptr(b, 16);                                   \
+                const lds_f* s16 = xv.xs16 + b * xv.ld16;                                            \
                 const float xs = s16[0] + s16[1];                                                    \
-                _Pragma("unroll") for (int r = 0; r < R; ++r) acc[r][b] += small_dot<T>(w[r], x, xs); \
+                _Pragma("unroll") for (int r = 0; r < R; ++r)                                        \
+                    acc[r][b] += small_dot<T>(w[r], x0, x16, xs);                                    \
             }                                                                                        \
         }                                                                                            \
     };
 
-template <int T, int N>
-__device__ __forceinline__ float small_dot(const uint32_t (&w)[N], const float* x, float xs);
 
 // Q4_0: d | qs[16]; d * (q - 8).  native.c:281-288
-template <>
-__device__ __forceinline__ float small_dot<T_Q4_0, 5>(const uint32_t (&w)[5], const float* x, float xs) {
+template <typename PX>
+__device__ __forceinline__ float small_dot_T_Q4_0(const uint32_t (&w)[5], PX x, PX x16, float xs) {
     uint32_t lo[4], hi[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -351,12 +375,12 @@ __device__ __forceinline__ float small_dot<T_Q4_0, 5>(const uint32_t (&w)[5], co
         lo[k] = oand(v, 0x0F0F0F0Fu);
         hi[k] = oand(v, 0xF0F0F0F0u);
     }
-    const float s = dot_run<4>(lo, x) + 0.0625f * dot_run<4>(hi, x + 16);
+    const float s = dot_run<4>(lo, x) + 0.0625f * dot_run<4>(hi, x16);
     return half_bits_to_float(w[0]) * (s - 8.f * xs);
 }
 // IQ4_NL: d | qs[16]; d * K[n].  native.c:351-358
-template <>
-__device__ __forceinline__ float small_dot<T_IQ4_NL, 5>(const uint32_t (&w)[5], const float* x, float xs) {
+template <typename PX>
+__device__ __forceinline__ float small_dot_T_IQ4_NL(const uint32_t (&w)[5], PX x, PX x16, float xs) {
     uint32_t lo[4], hi[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -364,24 +388,24 @@ __device__ __forceinline__ float small_dot<T_IQ4_NL, 5>(const uint32_t (&w)[5], 
         lo[k] = iq4_lut4(v & 0x0F0F0F0Fu);
         hi[k] = iq4_lut4((v >> 4) & 0x0F0F0F0Fu);
     }
-    const float s = dot_run<4>(lo, x) + dot_run<4>(hi, x + 16);
+    const float s = dot_run<4>(lo, x) + dot_run<4>(hi, x16);
     return half_bits_to_float(w[0]) * (s - 128.f * xs);
 }
 // Q4_1: d | m | qs[16]; d*q + m.  native.c:290-298
-template <>
-__device__ __forceinline__ float small_dot<T_Q4_1, 5>(const uint32_t (&w)[5], const float* x, float xs) {
+template <typename PX>
+__device__ __forceinline__ float small_dot_T_Q4_1(const uint32_t (&w)[5], PX x, PX x16, float xs) {
     uint32_t lo[4], hi[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         lo[k] = oand(w[1 + k], 0x0F0F0F0Fu);
         hi[k] = oand(w[1 + k], 0xF0F0F0F0u);
     }
-    const float s = dot_run<4>(lo, x) + 0.0625f * dot_run<4>(hi, x + 16);
+    const float s = dot_run<4>(lo, x) + 0.0625f * dot_run<4>(hi, x16);
     return half_bits_to_float(w[0]) * s + half_bits_to_float(w[0] >> 16) * xs;
 }
 // Q5_0: d | qh | qs[16]; d * (q5 - 16).  native.c:300-314
-template <>
-__device__ __forceinline__ float small_dot<T_Q5_0, 6>(const uint32_t (&w)[6], const float* x, float xs) {
+template <typename PX>
+__device__ __forceinline__ float small_dot_T_Q5_0(const uint32_t (&w)[6], PX x, PX x16, float xs) {
     const uint32_t qh = at_off(w, 0, 2);
     uint32_t lo[4], hi[4];
 #pragma unroll
@@ -390,12 +414,12 @@ __device__ __forceinline__ float small_dot<T_Q5_0, 6>(const uint32_t (&w)[6], co
         lo[k] = oandor(v, 0x0F0F0F0Fu, spread4(qh >> (4 * k)) << 4);
         hi[k] = oandor(v >> 4, 0x0F0F0F0Fu, spread4(qh >> (16 + 4 * k)) << 4);
     }
-    const float s = dot_run<4>(lo, x) + dot_run<4>(hi, x + 16);
+    const float s = dot_run<4>(lo, x) + dot_run<4>(hi, x16);
     return half_bits_to_float(w[0]) * (s - 16.f * xs);
 }
 // Q5_1: d | m | qh | qs[16]; d*q5 + m.  native.c:316-328
-template <>
-__device__ __forceinline__ float small_dot<T_Q5_1, 6>(const uint32_t (&w)[6], const float* x, float xs) {
+template <typename PX>
+__device__ __forceinline__ float small_dot_T_Q5_1(const uint32_t (&w)[6], PX x, PX x16, float xs) {
     const uint32_t qh = w[1];
     uint32_t lo[4], hi[4];
 #pragma unroll
@@ -404,12 +428,12 @@ __device__ __forceinline__ float small_dot<T_Q5_1, 6>(const uint32_t (&w)[6], co
         lo[k] = oandor(v, 0x0F0F0F0Fu, spread4(qh >> (4 * k)) << 4);
         hi[k] = oandor(v >> 4, 0x0F0F0F0Fu, spread4(qh >> (16 + 4 * k)) << 4);
     }
-    const float s = dot_run<4>(lo, x) + dot_run<4>(hi, x + 16);
+    const float s = dot_run<4>(lo, x) + dot_run<4>(hi, x16);
     return half_bits_to_float(w[0]) * s + half_bits_to_float(w[0] >> 16) * xs;
 }
 // Q8_0: d | i8 qs[32]; codes biased by +128 (xor 0x80) for unsigned conversion.  native.c:330-336
-template <>
-__device__ __forceinline__ float small_dot<T_Q8_0, 9>(const uint32_t (&w)[9], const float* x, float xs) {
+template <typename PX>
+__device__ __forceinline__ float small_dot_T_Q8_0(const uint32_t (&w)[9], PX x, PX x16, float xs) {
     uint32_t c[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) c[k] = at_off(w, k, 2) ^ 0x80808080u;
@@ -417,13 +441,25 @@ __device__ __forceinline__ float small_dot<T_Q8_0, 9>(const uint32_t (&w)[9], co
     return half_bits_to_float(w[0]) * (s - 128.f * xs);
 }
 // Q8_1: d | s | i8 qs[32].  native.c:338-344
-template <>
-__device__ __forceinline__ float small_dot<T_Q8_1, 9>(const uint32_t (&w)[9], const float* x, float xs) {
+template <typename PX>
+__device__ __forceinline__ float small_dot_T_Q8_1(const uint32_t (&w)[9], PX x, PX x16, float xs) {
     uint32_t c[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) c[k] = w[1 + k] ^ 0x80808080u;
     const float s = dot_run<8>(c, x);
     return half_bits_to_float(w[0]) * (s - 128.f * xs);
+}
+
+template <int T, int N, typename PX>
+__device__ __forceinline__ float small_dot(const uint32_t (&w)[N], PX x, PX x16, float xs) {
+    if constexpr (T == T_Q4_0) return small_dot_T_Q4_0(w, x, x16, xs);
+    if constexpr (T == T_IQ4_NL) return small_dot_T_IQ4_NL(w, x, x16, xs);
+    if constexpr (T == T_Q4_1) return small_dot_T_Q4_1(w, x, x16, xs);
+    if constexpr (T == T_Q5_0) return small_dot_T_Q5_0(w, x, x16, xs);
+    if constexpr (T == T_Q5_1) return small_dot_T_Q5_1(w, x, x16, xs);
+    if constexpr (T == T_Q8_0) return small_dot_T_Q8_0(w, x, x16, xs);
+    if constexpr (T == T_Q8_1) return small_dot_T_Q8_1(w, x, x16, xs);
+    return 0.f;
 }
 
 PYRITE_SMALL_UNIT(T_Q4_0)

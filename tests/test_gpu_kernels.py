@@ -218,3 +218,57 @@ def test_grouped_matvec_equals_single_launches(torch_dev, t, batch):
         for b in range(batch):
             ref = o.matvec(t, payload, x[b].astype(np.float64), rows, cols)
             assert_matvec_close(got[b], ref, x[b], rowmax, f"grouped {i} b{b}")
+
+
+QUANT_TYPES = [t for t in ALL_TYPES if TYPES[t][1] > 1]
+
+
+def _random_payload(t, rows, cols, seed):
+    """Random block bytes (every code, scale and bit pattern) with the fp16
+    block scale words kept finite, as in the reference's own kernel test."""
+    from tests.golden.make_golden import random_payload
+
+    return random_payload(np.random.default_rng(seed), t, rows, cols)
+
+
+@pytest.mark.parametrize("batch", [1, 5, 8])
+@pytest.mark.parametrize("t", QUANT_TYPES, ids=lambda t: TYPES[t][0])
+def test_device_matvec_random_payloads(torch_dev, t, batch):
+    torch = torch_dev
+    from pyrite_amd import device
+
+    o = oracle()
+    rows, cols = 70, 1024
+    payload = _random_payload(t, rows, cols, 4400 + t)
+    announce("device_matvec_random", TYPES[t][0], rows, cols, batch)
+    xs = np.stack([o.normal(4500 + b, cols) for b in range(batch)]).astype(np.float32)
+    y = device.matvec(t, device.upload(payload.tobytes()), torch.from_numpy(xs).cuda(), rows, cols).cpu().numpy()
+    wd = o.dequantize_rows(t, payload, rows, cols).reshape(rows, cols)
+    rowmax = np.abs(wd).max(axis=1)
+    for b in range(batch):
+        ref = o.matvec(t, payload, xs[b].astype(np.float64), rows, cols)
+        assert_matvec_close(y[b], ref, xs[b], rowmax, f"{TYPES[t][0]} random b{b}/{batch}")
+
+
+@pytest.mark.parametrize("cols,batch", [(1024, 1), (1024, 8), (4096, 8)])
+@pytest.mark.parametrize("t", [12, 14, 2, 8], ids=lambda t: TYPES[t][0])
+def test_device_matvec_large_activations(torch_dev, t, cols, batch):
+    """Activations beyond the fp16 range (|x| up to 3e6) are rescaled by a
+    power of two per vector; with 4096 columns at batch 8 the activations are
+    staged in several LDS chunks."""
+    torch = torch_dev
+    from pyrite_amd import device
+
+    o = oracle()
+    rows = 40
+    payload = _weights(t, rows, cols, 4600 + cols)
+    rng = np.random.default_rng(cols + batch)
+    xs = (rng.standard_normal((batch, cols)) * np.where(rng.random((batch, cols)) < 0.01, 1e6, 1.0)).astype(np.float32)
+    xs[0, 3] = 3.0e6
+    announce("device_matvec_large_x", TYPES[t][0], rows, cols, batch)
+    y = device.matvec(t, device.upload(payload.tobytes()), torch.from_numpy(xs).cuda(), rows, cols).cpu().numpy()
+    wd = o.dequantize_rows(t, payload, rows, cols).reshape(rows, cols)
+    rowmax = np.abs(wd).max(axis=1)
+    for b in range(batch):
+        ref = o.matvec(t, payload, xs[b].astype(np.float64), rows, cols)
+        assert_matvec_close(y[b], ref, xs[b], rowmax, f"{TYPES[t][0]} large-x b{b}/{batch}")
