@@ -187,4 +187,32 @@ __device__ __forceinline__ uint32_t spread4(uint32_t v) {
     return ((v & 0xFu) * 0x00204081u) & 0x01010101u;
 }
 
+// ---------------------------------------------------------------- lane sums
+// GFX9 DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1]
+// (lane ^ 2), row_half_mirror (lane i <-> 7 - i inside 8), row_mirror
+// (lane i <-> 15 - i inside 16).  Applied in this order each step pairs a lane
+// with one from the other half of its aligned group, so after step k every
+// lane holds the sum over its aligned group of 2^k lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each aligned group of 2^lg lanes (lg wave-uniform, 0..6) for every
+// element of v; every lane of a group receives the group sum.
+template <int R, int B>
+__device__ __forceinline__ void group_sum(float (&v)[R][B], int lg) {
+#define PYRITE_ALL(expr)                                      \
+    _Pragma("unroll") for (int r = 0; r < R; ++r)             \
+        _Pragma("unroll") for (int b = 0; b < B; ++b) expr;
+    if (lg >= 1) PYRITE_ALL(v[r][b] += dpp_f<0xB1>(v[r][b]))
+    if (lg >= 2) PYRITE_ALL(v[r][b] += dpp_f<0x4E>(v[r][b]))
+    if (lg >= 3) PYRITE_ALL(v[r][b] += dpp_f<0x141>(v[r][b]))
+    if (lg >= 4) PYRITE_ALL(v[r][b] += dpp_f<0x140>(v[r][b]))
+    // ds_swizzle bit mode inside 32 lanes: and_mask 0x1F, xor_mask 0x10
+    if (lg >= 5) PYRITE_ALL(v[r][b] += __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v[r][b]), 0x401F)))
+    if (lg >= 6) PYRITE_ALL(v[r][b] += __shfl_xor(v[r][b], 32, 64))
+#undef PYRITE_ALL
+}
+
 }  // namespace pyrite

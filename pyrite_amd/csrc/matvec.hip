@@ -15,6 +15,7 @@
 // minimum or code offset) are built once per workgroup in LDS.
 #include <hip/hip_ext.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include <type_traits>
 
@@ -49,80 +50,153 @@ struct MvGroup {
 
 // XL: activations staged in LDS (padded, see XView) instead of read from
 // global memory by every unit; used when B * cols fits the LDS budget.
-template <int T, int B, bool AL, bool XL>
+template <int T, int B, int R, bool AL, bool XL>
 __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* smem) {
-    constexpr int R = (B <= 2) ? 2 : 1;
     constexpr int BS = Geo<T>::bs, BPB = Geo<T>::bpb;
     const uint8_t* __restrict__ W = d.W;
     const float* __restrict__ X = d.X;
     const int rows = d.rows, cols = d.cols, lpr_log2 = d.lpr_log2;
     const unsigned long long ldx = d.ldx;
     const int n16 = cols >> 4;
-    lds_f* xs16 = (lds_f*)(smem);  // address-space cast: smem is LDS
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int LPR = 1 << lpr_log2, nslot = 64 >> lpr_log2;
+    const int slot = lane >> lpr_log2, li = lane & (LPR - 1);
+    const long long rows_per_wg = 4LL * nslot * R;
+    const long long wave_rows = (long long)nslot * R;
+    const long long stride_rows = (long long)d.wg_count * rows_per_wg;  // rows between row groups of this workgroup
+    long long wrow0 = (wg * 4 + wave) * wave_rows;                        // first row of this wave (wave-uniform)
+    long long row0 = wrow0 + (long long)slot * R;                         // first row of this lane's slot
+
+    float acc[R][B];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int b = 0; b < B; ++b) acc[r][b] = 0.f;
+
+    // reduce the slot's partial sums, store rows row0..row0+R-1, clear acc
+    auto flush = [&](long long r0) {
+        group_sum(acc, lpr_log2);
+        if (li == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (r0 + r < rows)
+#pragma unroll
+                    for (int b = 0; b < B; ++b) d.Y[b * d.ldy + r0 + r] = acc[r][b];
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int b = 0; b < B; ++b) acc[r][b] = 0.f;
+    };
+
     if constexpr (BS > 1) {
+        // Software pipeline over the lane's (row group, unit) sequence: the
+        // next unit's weights (possibly of the next row group) are loaded
+        // before the current unit is decoded, so every lane keeps two units
+        // of loads in flight.  The unit count per row group is wave-uniform
+        // (KU), which keeps the reduction converged.
+        using Un = Unit<T>;
+        using Raw = typename Un::Raw;
+        constexpr int P = Un::P;
+        static_assert((P & (P - 1)) == 0, "units per block must be a power of two");
+        constexpr int PL = P == 4 ? 2 : 0;
+        constexpr int PADI = Un::PADI;
+        const int U = (cols / BS) * P;
+        const int KU = (U + LPR - 1) >> lpr_log2;
+        // Row pointers (clamped to the last row) of the current and the next row group.
+        auto row_ptrs = [&](long long r0, const uint8_t* (&rp)[R]) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const long long rr = (r0 + r < rows) ? r0 + r : (long long)rows - 1;
+                rp[r] = W + rr * d.row_bytes;
+            }
+        };
+        const uint8_t* rp_cur[R];
+        const uint8_t* rp_nxt[R];
+        row_ptrs(row0, rp_cur);
+        row_ptrs(row0 + stride_rows, rp_nxt);
+        // Loads are issued unconditionally (unit index clamped to the row's
+        // last unit, rows clamped to the last row) so that every path through
+        // the loop has the same number of loads in flight and the waits before
+        // a decode cover only the older loads.
+        auto load_item = [&](Raw (&dst)[R], const uint8_t* const (&rp)[R], int u) {
+            const unsigned uu = (unsigned)(u < U ? u : U - 1);
+            const unsigned blk = uu >> PL, part = uu & (P - 1);
+#pragma unroll
+            for (int r = 0; r < R; ++r) Un::template load<AL>(rp[r] + (size_t)blk * BPB, (int)part, dst[r]);
+        };
+        Raw ra[R], rb[R];
+        load_item(ra, rp_cur, li);  // first weights in flight while the activations are staged
+
+        // Per-16-column sums of X (and, with XL, the padded copy of X) in LDS, one pass.
+        lds_f* xs16 = (lds_f*)(smem);  // address-space cast: smem is LDS
+        const int ldxl = cols + (cols / PADI) * 4;
+        lds_f* xl = xs16 + ((B * n16 + 3) & ~3);
         for (int i = threadIdx.x; i < B * n16; i += blockDim.x) {
             const int b = i / n16, j = i - b * n16;
             const float* p = X + b * ldx + 16 * j;
             const float4 a = ld_x4(p), c = ld_x4(p + 4), e = ld_x4(p + 8), f = ld_x4(p + 12);
             xs16[i] = (((a.x + a.y) + (a.z + a.w)) + ((c.x + c.y) + (c.z + c.w))) +
                       (((e.x + e.y) + (e.z + e.w)) + ((f.x + f.y) + (f.z + f.w)));
-        }
-    }
-    constexpr int PADI = [] {
-        if constexpr (BS > 1) return Unit<T>::PADI;
-        else return 32;
-    }();
-    const int ldxl = cols + (cols / PADI) * 4;
-    lds_f* xl = xs16 + ((B * n16 + 3) & ~3);
-    if constexpr (XL) {
-        const int q = cols >> 2;
-        for (int i = threadIdx.x; i < B * q; i += blockDim.x) {
-            const int b = i / q, e = (i - b * q) * 4;
-            st_x4(xl + b * ldxl + e + (e / PADI) * 4, ld_x4(X + b * ldx + e));
-        }
-    }
-    if constexpr (BS > 1) __syncthreads();
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int LPR = 1 << lpr_log2, nslot = 64 >> lpr_log2;
-    const int slot = lane >> lpr_log2, li = lane & (LPR - 1);
-    const long long rows_per_wg = 4LL * nslot * R;
-    for (long long rg = wg; rg * rows_per_wg < rows; rg += d.wg_count) {
-        const long long wave_row0 = (rg * 4 + wave) * nslot * R;
-        if (wave_row0 >= rows) break;
-        const long long row0 = wave_row0 + (long long)slot * R;
-
-        float acc[R][B];
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int b = 0; b < B; ++b) acc[r][b] = 0.f;
-
-        const uint8_t* rp[R];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            const long long rr = (row0 + r < rows) ? row0 + r : (long long)rows - 1;
-            rp[r] = W + rr * d.row_bytes;
-        }
-
-        if constexpr (BS > 1) {
-            constexpr int P = Unit<T>::P;
-            const int U = (cols / BS) * P;
-            XView<XL, PADI> xv;
-            xv.ldx = XL ? (size_t)ldxl : (size_t)ldx;
-            xv.ld16 = n16;
-            for (int u = li; u < U; u += LPR) {
-                const int blk = u / P, part = u - blk * P;
-                const uint8_t* bp[R];
-#pragma unroll
-                for (int r = 0; r < R; ++r) bp[r] = rp[r] + (size_t)blk * BPB;
-                if constexpr (XL) xv.x = xl + blk * BS + (blk * BS / PADI) * 4;
-                else xv.x = X + (size_t)blk * BS;
-                xv.xs16 = xs16 + blk * (BS / 16);
-                Unit<T>::template run<B, R, AL>(bp, part, xv, acc);
+            if constexpr (XL) {
+                // 16 columns never straddle a pad (PADI is a multiple of 16)
+                lds_f* q = xl + b * ldxl + 16 * j + (16 * j / PADI) * 4;
+                st_x4(q, a); st_x4(q + 4, c); st_x4(q + 8, e); st_x4(q + 12, f);
             }
-        } else {
+        }
+        __syncthreads();
+        if (wrow0 >= rows) return;
+
+        XView<XL, PADI> xv;
+        xv.ldx = XL ? (size_t)ldxl : (size_t)ldx;
+        xv.ld16 = n16;
+        auto dot_item = [&](const Raw (&src)[R], int u) {
+            const unsigned blk = (unsigned)u >> PL, part = (unsigned)u & (P - 1);
+            if constexpr (XL) xv.x = xl + blk * BS + (blk * BS / PADI) * 4;
+            else xv.x = X + (size_t)blk * BS;
+            xv.xs16 = xs16 + blk * (BS / 16);
+            Un::template dot<B, R>(src, (int)part, xv, acc);
+        };
+        int k = 0;
+        // one pipeline step: decode cur (unit k), with unit k+1 loaded into nxt; true when done
+        auto step = [&](Raw (&cur)[R], Raw (&nxt)[R]) -> bool {
+            const int u = li + (k << lpr_log2);
+            const bool adv = (k + 1 == KU);
+            const int un = adv ? li : u + LPR;
+            const uint8_t* rpl[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) rpl[r] = adv ? rp_nxt[r] : rp_cur[r];
+            load_item(nxt, rpl, un);
+            if (u < U) dot_item(cur, u);
+            if (adv) {
+                flush(row0);
+                wrow0 += stride_rows;
+                if (wrow0 >= rows) return true;
+                row0 += stride_rows;
+#pragma unroll
+                for (int r = 0; r < R; ++r) rp_cur[r] = rp_nxt[r];
+                row_ptrs(row0 + stride_rows, rp_nxt);
+                k = 0;
+            } else {
+                ++k;
+            }
+            return false;
+        };
+        for (;;) {
+            if (step(ra, rb)) break;
+            if (step(rb, ra)) break;
+        }
+    } else {
+        if (wrow0 >= rows) return;
+        for (;;) {
             const int U = (cols + 3) >> 2;
+            const uint8_t* rp[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const long long rr = (row0 + r < rows) ? row0 + r : (long long)rows - 1;
+                rp[r] = W + rr * d.row_bytes;
+            }
             for (int u = li; u < U; u += LPR) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -137,30 +211,20 @@ __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* sm
                     }
                 }
             }
-        }
-
-        for (int off = LPR >> 1; off > 0; off >>= 1)
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int b = 0; b < B; ++b) acc[r][b] += __shfl_xor(acc[r][b], off, 64);
-
-        if (li == 0) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (row0 + r < rows)
-#pragma unroll
-                    for (int b = 0; b < B; ++b) d.Y[b * d.ldy + row0 + r] = acc[r][b];
+            flush(row0);
+            wrow0 += stride_rows;
+            if (wrow0 >= rows) break;
+            row0 += stride_rows;
         }
     }
 }
 
-template <int T, int B, bool AL, bool XL>
+template <int T, int B, int R, bool AL, bool XL>
 __global__ __launch_bounds__(256) void mv_kernel(const MvGroup g) {
     extern __shared__ float smem[];
     int i = 0;
     while (i + 1 < g.n && (int)blockIdx.x >= g.d[i + 1].wg_begin) ++i;
-    mv_body<T, B, AL, XL>(g.d[i], (long long)blockIdx.x - g.d[i].wg_begin, smem);
+    mv_body<T, B, R, AL, XL>(g.d[i], (long long)blockIdx.x - g.d[i].wg_begin, smem);
 }
 
 // ---------------------------------------------------------------- launcher
@@ -178,26 +242,155 @@ static long long units_per_row(int cols) {
     else return (cols + 3) / 4;
 }
 
-// Workgroups per launch to aim for: 8 per CU on a 256-CU MI355X.  A
-// workgroup loops over row groups, so the per-workgroup prologue (x sums in
-// LDS) is paid once per workgroup, not once per 8 rows.
-constexpr long long kTargetWgs = 2048;
+// A launch uses at most as many workgroups as the device holds at once
+// (persistent workgroups): each loops over row groups, so the per-workgroup
+// prologue (activations and their 16-column sums staged in LDS) is paid once
+// per resident workgroup instead of once per row group.
+struct DevInfo {
+    int cus;
+    size_t lds_per_cu;
+};
+static const DevInfo& dev_info() {
+    static const DevInfo info = [] {
+        DevInfo i{256, 160 * 1024};
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess) {
+            if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) i.cus = v;
+            if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) == hipSuccess && v > 0)
+                i.lds_per_cu = (size_t)v;
+        }
+        return i;
+    }();
+    return info;
+}
 
-// Fill lpr_log2 / wg_begin / wg_count for B and return the total number of
-// workgroups.  Each matrix gets workgroups in proportion to its weight bytes.
+// Workgroups of one kernel instance resident per CU, from its register use.
+template <int T, int B, int R, bool AL, bool XL>
+static int wgs_per_cu_regs() {
+    static const int n = [] {
+        int v = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, mv_kernel<T, B, R, AL, XL>, 256, 0) != hipSuccess || v < 1)
+            v = 1;
+        return v;
+    }();
+    return n;
+}
+
+// Optional tuning override "R,KU" (rows per slot, units per lane) from
+// PYRITE_MATVEC_SHAPE; 0 means "choose".
+struct ShapeOverride {
+    int r = 0, ku = 0;
+};
+static const ShapeOverride& shape_override() {
+    static const ShapeOverride o = [] {
+        ShapeOverride v;
+        const char* e = getenv("PYRITE_MATVEC_SHAPE");
+        if (e) {
+            v.r = atoi(e);
+            const char* c = strchr(e, ',');
+            if (c) v.ku = atoi(c + 1);
+        }
+        return v;
+    }();
+    return o;
+}
+
+// Slot geometry for one matrix: the largest units-per-lane KU (<= 8) whose
+// slots still give at least `target` waves, so the per-row-group cost (lane
+// reduction, row pointers, store) is spread over several units without
+// leaving resident waves idle.  Returns lpr_log2 and the waves it needs.
+static int plan_lpr(long long U, long long rows, int R, long long target, long long* waves_out) {
+    int best = -1;
+    long long best_w = 0;
+    const int forced = shape_override().ku;
+    for (int ku = 1; ku <= 8; ku *= 2) {
+        if (forced && ku != forced) continue;
+        const long long per_lane = (U + ku - 1) / ku;
+        const int lg = log2_ceil(per_lane < 64 ? per_lane : 64);
+        const long long rows_per_wave = (long long)(64 >> lg) * R;
+        const long long w = (rows + rows_per_wave - 1) / rows_per_wave;
+        if (best < 0 || forced || w >= target) { best = lg; best_w = w; }
+        if (w < target) break;
+    }
+    *waves_out = best_w;
+    return best;
+}
+
+template <int T, int B, int R, bool AL, bool XL>
+static long long resident_wgs(size_t lds) {
+    const DevInfo& di = dev_info();
+    long long per_cu = wgs_per_cu_regs<T, B, R, AL, XL>();
+    if (lds > 0 && (long long)(di.lds_per_cu / lds) < per_cu) per_cu = (long long)(di.lds_per_cu / lds);
+    if (per_cu < 1) per_cu = 1;
+    return per_cu * di.cus;
+}
+
+// LDS bytes of a launch: per-16-column sums, plus the padded activations when staged.
 template <int T, int B>
-static long long plan_group(MvGroup& g) {
-    const int R = (B <= 2) ? 2 : 1;
+static size_t lds_bytes(int max_cols, bool xl) {
+    if constexpr (Geo<T>::bs == 1) {
+        return 0;
+    } else {
+        size_t n = (size_t)B * (max_cols / 16) * sizeof(float);
+        if (xl) {
+            constexpr int PADI = Unit<T>::PADI;
+            n = ((n / sizeof(float) + 3) & ~size_t(3)) * sizeof(float) +
+                (size_t)B * (max_cols + (max_cols / PADI) * 4) * sizeof(float);
+        }
+        return n;
+    }
+}
+template <int T, int B>
+static bool use_xl(int max_cols) {
+    return Geo<T>::bs > 1 && B <= 2 && lds_bytes<T, B>(max_cols, true) <= 65536;
+}
+
+// Slot shape of one matrix (rows per slot R, lanes per row), a function of
+// the matrix and the device only, so a matrix gives bit-identical results
+// whether it is launched alone or in a group.  B == 1 uses two rows per slot
+// (every activation read serves both) unless that leaves resident waves idle.
+struct MatShape {
+    int R;
+    int lpr_log2;
+};
+template <int T, int B, bool AL>
+static MatShape mat_shape(int rows, int cols) {
+    const long long U = units_per_row<T>(cols);
+    const bool xl = use_xl<T, B>(cols);
+    const size_t lds = lds_bytes<T, B>(cols, xl);
+    int R = 1;
+    if constexpr (B == 1) {
+        const int forced = shape_override().r;
+        if (forced) {
+            R = forced == 2 ? 2 : 1;
+        } else {
+            long long w = 0;
+            plan_lpr(U, rows, 2, 1LL << 40, &w);  // waves at one unit per lane
+            const long long target = 4 * (xl ? resident_wgs<T, B, 2, AL, true>(lds) : resident_wgs<T, B, 2, AL, false>(lds));
+            R = (w >= target) ? 2 : 1;
+        }
+    }
+    long long target = 4 * (xl ? resident_wgs<T, B, 1, AL, true>(lds) : resident_wgs<T, B, 1, AL, false>(lds));
+    if constexpr (B == 1) {
+        if (R == 2) target = 4 * (xl ? resident_wgs<T, B, 2, AL, true>(lds) : resident_wgs<T, B, 2, AL, false>(lds));
+    }
+    long long w = 0;
+    return MatShape{R, plan_lpr(U, rows, R, target, &w)};
+}
+
+// Fill wg_begin / wg_count (lpr_log2 is already set) and return the total
+// number of workgroups (at most cap).  Each matrix gets workgroups in
+// proportion to its weight bytes, never more than it has row groups.
+static long long plan_group(MvGroup& g, int R, long long cap) {
     double total_bytes = 0;
     for (int i = 0; i < g.n; ++i) total_bytes += (double)g.d[i].rows * (double)g.d[i].row_bytes;
     long long wg = 0;
     for (int i = 0; i < g.n; ++i) {
-        const long long U = units_per_row<T>(g.d[i].cols);
-        g.d[i].lpr_log2 = log2_ceil(U < 64 ? U : 64);
+        const double frac = ((double)g.d[i].rows * (double)g.d[i].row_bytes) / (total_bytes > 0 ? total_bytes : 1.0);
+        long long share = (long long)((double)cap * frac);
+        if (share < 1) share = 1;
         const long long rows_per_wg = 4LL * (64 >> g.d[i].lpr_log2) * R;
         const long long need = (g.d[i].rows + rows_per_wg - 1) / rows_per_wg;
-        long long share = (long long)((double)kTargetWgs * ((double)g.d[i].rows * (double)g.d[i].row_bytes) /
-                                      (total_bytes > 0 ? total_bytes : 1.0)) + 1;
         const long long cnt = need < share ? need : share;
         g.d[i].wg_begin = (int)wg;
         g.d[i].wg_count = (int)cnt;
@@ -213,39 +406,63 @@ struct LaunchEvents {
     hipEvent_t stop = nullptr;
 };
 
-template <int T, int B, bool AL, bool XL>
-static hipError_t launch_group_x(const MvGroup& g, long long wgs, size_t lds, hipStream_t stream, LaunchEvents ev) {
+template <int T, int B, int R, bool AL, bool XL>
+static hipError_t launch_group_r(MvGroup g, size_t lds, hipStream_t stream, LaunchEvents ev) {
+    const long long wgs = plan_group(g, R, resident_wgs<T, B, R, AL, XL>(lds));
+    if (wgs <= 0 || wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
     if (ev.start || ev.stop)
-        hipExtLaunchKernelGGL((mv_kernel<T, B, AL, XL>), dim3((unsigned)wgs), dim3(256), (uint32_t)lds, stream,
+        hipExtLaunchKernelGGL((mv_kernel<T, B, R, AL, XL>), dim3((unsigned)wgs), dim3(256), (uint32_t)lds, stream,
                               ev.start, ev.stop, 0, g);
     else
-        hipLaunchKernelGGL((mv_kernel<T, B, AL, XL>), dim3((unsigned)wgs), dim3(256), lds, stream, g);
+        hipLaunchKernelGGL((mv_kernel<T, B, R, AL, XL>), dim3((unsigned)wgs), dim3(256), lds, stream, g);
     return hipGetLastError();
 }
 
+template <int T, int B, int R, bool AL>
+static hipError_t launch_group_rx(const MvGroup& g, hipStream_t stream, LaunchEvents ev) {
+    int max_cols = 0;
+    for (int i = 0; i < g.n; ++i) max_cols = g.d[i].cols > max_cols ? g.d[i].cols : max_cols;
+    if (use_xl<T, B>(max_cols))
+        return launch_group_r<T, B, R, AL, true>(g, lds_bytes<T, B>(max_cols, true), stream, ev);
+    return launch_group_r<T, B, R, AL, false>(g, lds_bytes<T, B>(max_cols, false), stream, ev);
+}
+
+// Split the group by rows-per-slot (one launch per R present).
 template <int T, int B, bool AL>
-static hipError_t launch_group(MvGroup g, size_t lds, hipStream_t stream, LaunchEvents ev) {
-    const long long wgs = plan_group<T, B>(g);
-    if (wgs <= 0 || wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
-    if constexpr (Geo<T>::bs > 1 && B <= 2) {
-        // stage the activations in LDS when they fit next to the column sums
-        constexpr int PADI = Unit<T>::PADI;
-        int max_cols = 0;
-        for (int i = 0; i < g.n; ++i) max_cols = g.d[i].cols > max_cols ? g.d[i].cols : max_cols;
-        const size_t xl = (size_t)B * (max_cols + (max_cols / PADI) * 4) * sizeof(float);
-        const size_t lds_x = ((lds / sizeof(float) + 3) & ~size_t(3)) * sizeof(float) + xl;
-        if (lds_x <= 65536) return launch_group_x<T, B, AL, true>(g, wgs, lds_x, stream, ev);
+static hipError_t launch_group(const MvGroup& g, hipStream_t stream, LaunchEvents ev) {
+    MvGroup by_r[2];
+    by_r[0].n = by_r[1].n = 0;
+    for (int i = 0; i < g.n; ++i) {
+        const MatShape sh = mat_shape<T, B, AL>(g.d[i].rows, g.d[i].cols);
+        MvDesc d = g.d[i];
+        d.lpr_log2 = sh.lpr_log2;
+        MvGroup& dst = by_r[sh.R - 1];
+        dst.d[dst.n++] = d;
     }
-    return launch_group_x<T, B, AL, false>(g, wgs, lds, stream, ev);
+    const int first = by_r[0].n ? 0 : 1, last = by_r[1].n ? 1 : 0;
+    for (int k = first; k <= last; ++k) {
+        if (by_r[k].n == 0) continue;
+        LaunchEvents e;
+        if (k == first) e.start = ev.start;
+        if (k == last) e.stop = ev.stop;
+        hipError_t err = hipSuccess;
+        if constexpr (B == 1) {
+            err = k ? launch_group_rx<T, B, 2, AL>(by_r[k], stream, e) : launch_group_rx<T, B, 1, AL>(by_r[k], stream, e);
+        } else {
+            err = launch_group_rx<T, B, 1, AL>(by_r[k], stream, e);
+        }
+        if (err != hipSuccess) return err;
+    }
+    return hipSuccess;
 }
 
 template <int T, bool AL>
-static hipError_t launch_type(int batch, const MvGroup& g, size_t lds, hipStream_t s, LaunchEvents ev) {
+static hipError_t launch_type(int batch, const MvGroup& g, hipStream_t s, LaunchEvents ev) {
     switch (batch) {
-    case 1: return launch_group<T, 1, AL>(g, lds, s, ev);
-    case 2: return launch_group<T, 2, AL>(g, lds, s, ev);
-    case 4: return launch_group<T, 4, AL>(g, lds, s, ev);
-    case 8: return launch_group<T, 8, AL>(g, lds, s, ev);
+    case 1: return launch_group<T, 1, AL>(g, s, ev);
+    case 2: return launch_group<T, 2, AL>(g, s, ev);
+    case 4: return launch_group<T, 4, AL>(g, s, ev);
+    case 8: return launch_group<T, 8, AL>(g, s, ev);
     default: return hipErrorInvalidValue;
     }
 }
@@ -292,7 +509,6 @@ int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch
             if (!quant || (size_t)cand * (max_cols / 16) * sizeof(float) <= 65536) { c = cand; break; }
         }
         if (c == 0) return -2;
-        const size_t lds = quant ? (size_t)c * (max_cols / 16) * sizeof(float) : 0;
         for (size_t base = 0; base < n; base += kMaxGroup) {
             LaunchEvents ev;
             if (done == 0 && base == 0) ev.start = start;
@@ -314,8 +530,8 @@ int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch
             hipError_t e = hipSuccess;
 #define PYRITE_CASE(T)                                                                       \
     case T:                                                                                \
-        e = al ? launch_type<T, (Geo<T>::bpb % 4 == 0)>(c, grp, lds, stream, ev)           \
-               : launch_type<T, false>(c, grp, lds, stream, ev);                           \
+        e = al ? launch_type<T, (Geo<T>::bpb % 4 == 0)>(c, grp, stream, ev)                \
+               : launch_type<T, false>(c, grp, stream, ev);                                \
         break;
             switch (type) {
                 PYRITE_FOR_EACH_TYPE(PYRITE_CASE)

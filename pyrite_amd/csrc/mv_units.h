@@ -82,30 +82,29 @@ __device__ __forceinline__ void k4_pair_regs(uint32_t s0, uint32_t s1, uint32_t 
 
 template <> struct Unit<T_Q4_K> {
     static constexpr int P = 4, PADI = 64;
-    template <int B, int R, bool AL, class XV>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int c, const XV& xv,
+    struct Raw { uint32_t hd[4]; uint32_t q[8]; };
+    template <bool AL>
+    __device__ __forceinline__ static void load(const uint8_t* blk, int c, Raw& raw) {
+        ld_span<16, AL>(blk, raw.hd);
+        ld_span<32, AL>(blk + 16 + 32 * c, raw.q);
+    }
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void dot(const Raw (&raw)[R], int c, const XV& xv,
                                                float (&acc)[R][B]) {
-        uint32_t hd[R][4], q[R][8];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            ld_span<16, AL>(blk[r], hd[r]);
-            ld_span<32, AL>(blk[r] + 16 + 32 * c, q[r]);
-        }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const auto x = xv.ptr(b, 64 * c), xh = xv.ptr(b, 64 * c + 32);
             const lds_f* s16 = xv.xs16 + b * xv.ld16 + 4 * c;
             const float xlo = s16[0] + s16[1], xhi = s16[2] + s16[3];
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 uint32_t lo[8], hi[8];
 #pragma unroll
-                for (int k = 0; k < 8; ++k) { lo[k] = oand(q[r][k], 0x0F0F0F0Fu); hi[k] = oand(q[r][k], 0xF0F0F0F0u); }
-                const float slo = dot_run<8>(lo, x);
-                const float shi = dot_run<8>(hi, xh);
+                for (int k = 0; k < 8; ++k) { lo[k] = oand(raw[r].q[k], 0x0F0F0F0Fu); hi[k] = oand(raw[r].q[k], 0xF0F0F0F0u); }
+                const float slo = dot_run<8>(lo, xv.ptr(b, 64 * c));
+                const float shi = dot_run<8>(hi, xv.ptr(b, 64 * c + 32));
                 float sc0, m0, sc1, m1;
-                k4_pair_regs(hd[r][1], hd[r][2], hd[r][3], c, sc0, m0, sc1, m1);
-                const float d = half_bits_to_float(hd[r][0]), dmin = half_bits_to_float(hd[r][0] >> 16);
+                k4_pair_regs(raw[r].hd[1], raw[r].hd[2], raw[r].hd[3], c, sc0, m0, sc1, m1);
+                const float d = half_bits_to_float(raw[r].hd[0]), dmin = half_bits_to_float(raw[r].hd[0] >> 16);
                 acc[r][b] += d * (sc0 * slo + sc1 * 0.0625f * shi) - dmin * (m0 * xlo + m1 * xhi);
             }
         }
@@ -116,16 +115,16 @@ template <> struct Unit<T_Q4_K> {
 // as Q4_K plus a fifth bit: qh[l] bit 2c (low) / 2c+1 (high).  native.c:410-437
 template <> struct Unit<T_Q5_K> {
     static constexpr int P = 4, PADI = 64;
-    template <int B, int R, bool AL, class XV>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int c, const XV& xv,
+    struct Raw { uint32_t hd[4]; uint32_t q[8]; uint32_t h[8]; };
+    template <bool AL>
+    __device__ __forceinline__ static void load(const uint8_t* blk, int c, Raw& raw) {
+        ld_span<16, AL>(blk, raw.hd);
+        ld_span<32, AL>(blk + 16, raw.h);
+        ld_span<32, AL>(blk + 48 + 32 * c, raw.q);
+    }
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void dot(const Raw (&raw)[R], int c, const XV& xv,
                                                float (&acc)[R][B]) {
-        uint32_t hd[R][4], q[R][8], h[R][8];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            ld_span<16, AL>(blk[r], hd[r]);
-            ld_span<32, AL>(blk[r] + 16, h[r]);
-            ld_span<32, AL>(blk[r] + 48 + 32 * c, q[r]);
-        }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const auto x = xv.ptr(b, 64 * c), xh = xv.ptr(b, 64 * c + 32);
@@ -136,14 +135,14 @@ template <> struct Unit<T_Q5_K> {
                 uint32_t lo[8], hi[8];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) {
-                    lo[k] = oandor(q[r][k], 0x0F0F0F0Fu, ((h[r][k] >> (2 * c)) & 0x01010101u) << 4);
-                    hi[k] = oandor(q[r][k] >> 4, 0x0F0F0F0Fu, ((h[r][k] >> (2 * c + 1)) & 0x01010101u) << 4);
+                    lo[k] = oandor(raw[r].q[k], 0x0F0F0F0Fu, ((raw[r].h[k] >> (2 * c)) & 0x01010101u) << 4);
+                    hi[k] = oandor(raw[r].q[k] >> 4, 0x0F0F0F0Fu, ((raw[r].h[k] >> (2 * c + 1)) & 0x01010101u) << 4);
                 }
                 const float slo = dot_run<8>(lo, x);
                 const float shi = dot_run<8>(hi, xh);
                 float sc0, m0, sc1, m1;
-                k4_pair_regs(hd[r][1], hd[r][2], hd[r][3], c, sc0, m0, sc1, m1);
-                const float d = half_bits_to_float(hd[r][0]), dmin = half_bits_to_float(hd[r][0] >> 16);
+                k4_pair_regs(raw[r].hd[1], raw[r].hd[2], raw[r].hd[3], c, sc0, m0, sc1, m1);
+                const float d = half_bits_to_float(raw[r].hd[0]), dmin = half_bits_to_float(raw[r].hd[0] >> 16);
                 acc[r][b] += d * (sc0 * slo + sc1 * shi) - dmin * (m0 * xlo + m1 * xhi);
             }
         }
@@ -156,19 +155,20 @@ template <> struct Unit<T_Q5_K> {
 // g >> 1; qh byte 32h+16r'+l bits 2g; scale 8h + 2g + r'.  native.c:199-225
 template <> struct Unit<T_Q6_K> {
     static constexpr int P = 4, PADI = 128;
-    template <int B, int R, bool AL, class XV>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XV& xv,
+    struct Raw { uint32_t A[4]; uint32_t Bq[4]; uint32_t H[4]; uint32_t S[2]; uint32_t D[1]; };
+    template <bool AL>
+    __device__ __forceinline__ static void load(const uint8_t* blk, int u, Raw& raw) {
+        const int h = u >> 1, rr = u & 1;
+        ld_span<16, AL>(blk + 64 * h + 16 * rr, raw.A);
+        ld_span<16, AL>(blk + 64 * h + 32 + 16 * rr, raw.Bq);
+        ld_span<16, AL>(blk + 128 + 32 * h + 16 * rr, raw.H);
+        ld_span<8, AL>(blk + 192 + 8 * h, raw.S);
+        ld_span<2, AL>(blk + 208, raw.D);
+    }
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void dot(const Raw (&raw)[R], int u, const XV& xv,
                                                float (&acc)[R][B]) {
         const int h = u >> 1, rr = u & 1;
-        uint32_t A[R][4], Bq[R][4], H[R][4], S[R][2], D[R][1];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            ld_span<16, AL>(blk[r] + 64 * h + 16 * rr, A[r]);
-            ld_span<16, AL>(blk[r] + 64 * h + 32 + 16 * rr, Bq[r]);
-            ld_span<16, AL>(blk[r] + 128 + 32 * h + 16 * rr, H[r]);
-            ld_span<8, AL>(blk[r] + 192 + 8 * h, S[r]);
-            ld_span<2, AL>(blk[r] + 208, D[r]);
-        }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const int xo = 128 * h + 16 * rr;
@@ -181,16 +181,16 @@ template <> struct Unit<T_Q6_K> {
                     uint32_t c[4];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
-                        const uint32_t lq = (g & 1) ? Bq[r][k] : A[r][k];
+                        const uint32_t lq = (g & 1) ? raw[r].Bq[k] : raw[r].A[k];
                         c[k] = oandor((g & 2) ? (lq >> 4) : lq, 0x0F0F0F0Fu,
-                                      ((H[r][k] >> (2 * g)) & 0x03030303u) << 4);
+                                      ((raw[r].H[k] >> (2 * g)) & 0x03030303u) << 4);
                     }
                     const float sg = dot_run<4>(c, xv.ptr(b, xo + 32 * g));
-                    const uint32_t sw = S[r][g >> 1] >> (8 * (rr + 2 * (g & 1)));
+                    const uint32_t sw = raw[r].S[g >> 1] >> (8 * (rr + 2 * (g & 1)));
                     const float sc = (float)(int)(int8_t)(sw & 0xFF);
                     tot += sc * (sg - 32.f * s16[2 * g]);
                 }
-                acc[r][b] += half_bits_to_float(D[r][0]) * tot;
+                acc[r][b] += half_bits_to_float(raw[r].D[0]) * tot;
             }
         }
     }
@@ -202,17 +202,18 @@ template <> struct Unit<T_Q6_K> {
 // high nibble min); d, dmin at 80, 82.  native.c:381-408
 template <> struct Unit<T_Q2_K> {
     static constexpr int P = 4, PADI = 128;
-    template <int B, int R, bool AL, class XV>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XV& xv,
+    struct Raw { uint32_t Q[4]; uint32_t S[2]; uint32_t D[1]; };
+    template <bool AL>
+    __device__ __forceinline__ static void load(const uint8_t* blk, int u, Raw& raw) {
+        const int h = u >> 1, rr = u & 1;
+        ld_span<16, AL>(blk + 16 + 32 * h + 16 * rr, raw.Q);
+        ld_span<8, AL>(blk + 8 * h, raw.S);
+        ld_span<4, AL>(blk + 80, raw.D);
+    }
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void dot(const Raw (&raw)[R], int u, const XV& xv,
                                                float (&acc)[R][B]) {
         const int h = u >> 1, rr = u & 1;
-        uint32_t Q[R][4], S[R][2], D[R][1];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            ld_span<16, AL>(blk[r] + 16 + 32 * h + 16 * rr, Q[r]);
-            ld_span<8, AL>(blk[r] + 8 * h, S[r]);
-            ld_span<4, AL>(blk[r] + 80, D[r]);
-        }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const int xo = 128 * h + 16 * rr;
@@ -224,13 +225,13 @@ template <> struct Unit<T_Q2_K> {
                 for (int g = 0; g < 4; ++g) {
                     uint32_t c[4];
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) c[k] = oand(Q[r][k] >> (2 * g), 0x03030303u);
+                    for (int k = 0; k < 4; ++k) c[k] = oand(raw[r].Q[k] >> (2 * g), 0x03030303u);
                     const float sg = dot_run<4>(c, xv.ptr(b, xo + 32 * g));
-                    const uint32_t sb = (S[r][g >> 1] >> (8 * (rr + 2 * (g & 1)))) & 0xFF;
+                    const uint32_t sb = (raw[r].S[g >> 1] >> (8 * (rr + 2 * (g & 1)))) & 0xFF;
                     ts += (float)(sb & 15) * sg;
                     tm += (float)(sb >> 4) * s16[2 * g];
                 }
-                acc[r][b] += half_bits_to_float(D[r][0]) * ts - half_bits_to_float(D[r][0] >> 16) * tm;
+                acc[r][b] += half_bits_to_float(raw[r].D[0]) * ts - half_bits_to_float(raw[r].D[0] >> 16) * tm;
             }
         }
     }
@@ -242,18 +243,19 @@ template <> struct Unit<T_Q2_K> {
 // 12 packed bytes at 96, d at 108.  native.c:129-171
 template <> struct Unit<T_Q3_K> {
     static constexpr int P = 4, PADI = 128;
-    template <int B, int R, bool AL, class XV>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XV& xv,
+    struct Raw { uint32_t Q[4]; uint32_t M[4]; uint32_t S[3]; uint32_t D[1]; };
+    template <bool AL>
+    __device__ __forceinline__ static void load(const uint8_t* blk, int u, Raw& raw) {
+        const int h = u >> 1, rr = u & 1;
+        ld_span<16, AL>(blk + 32 + 32 * h + 16 * rr, raw.Q);
+        ld_span<16, AL>(blk + 16 * rr, raw.M);
+        ld_span<12, AL>(blk + 96, raw.S);
+        ld_span<2, AL>(blk + 108, raw.D);
+    }
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void dot(const Raw (&raw)[R], int u, const XV& xv,
                                                float (&acc)[R][B]) {
         const int h = u >> 1, rr = u & 1;
-        uint32_t Q[R][4], M[R][4], S[R][3], D[R][1];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            ld_span<16, AL>(blk[r] + 32 + 32 * h + 16 * rr, Q[r]);
-            ld_span<16, AL>(blk[r] + 16 * rr, M[r]);
-            ld_span<12, AL>(blk[r] + 96, S[r]);
-            ld_span<2, AL>(blk[r] + 108, D[r]);
-        }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const int xo = 128 * h + 16 * rr;
@@ -266,19 +268,19 @@ template <> struct Unit<T_Q3_K> {
                     uint32_t c[4];
 #pragma unroll
                     for (int k = 0; k < 4; ++k)
-                        c[k] = oandor(Q[r][k] >> (2 * g), 0x03030303u,
-                                      ((M[r][k] >> (4 * h + g)) & 0x01010101u) << 2);
+                        c[k] = oandor(raw[r].Q[k] >> (2 * g), 0x03030303u,
+                                      ((raw[r].M[k] >> (4 * h + g)) & 0x01010101u) << 2);
                     const float sg = dot_run<4>(c, xv.ptr(b, xo + 32 * g));
                     // j = 8h + 2g + r': low nibble from byte 2g + r' (h selects the nibble),
                     // top two bits from byte 8 + (2g + r') % 4 at bit 2 * (2h + g / 2)
-                    const uint32_t lb = (S[r][g >> 1] >> (8 * (rr + 2 * (g & 1)))) & 0xFF;
+                    const uint32_t lb = (raw[r].S[g >> 1] >> (8 * (rr + 2 * (g & 1)))) & 0xFF;
                     const uint32_t low4 = h ? (lb >> 4) : (lb & 15);
-                    const uint32_t hb = (S[r][2] >> (8 * ((2 * g + rr) & 3))) & 0xFF;
+                    const uint32_t hb = (raw[r].S[2] >> (8 * ((2 * g + rr) & 3))) & 0xFF;
                     const uint32_t hi2 = (hb >> (2 * (2 * h + (g >> 1)))) & 3;
                     const float sc = (float)(int)(low4 | (hi2 << 4)) - 32.f;
                     tot += sc * (sg - 4.f * s16[2 * g]);
                 }
-                acc[r][b] += half_bits_to_float(D[r][0]) * tot;
+                acc[r][b] += half_bits_to_float(raw[r].D[0]) * tot;
             }
         }
     }
@@ -290,22 +292,22 @@ template <> struct Unit<T_Q3_K> {
 // d*(ls-32)*K[n].  native.c:364-379
 template <> struct Unit<T_IQ4_XS> {
     static constexpr int P = 4, PADI = 64;
-    template <int B, int R, bool AL, class XV>
-    __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int u, const XV& xv,
+    struct Raw { uint32_t hd[2]; uint32_t q[8]; };
+    template <bool AL>
+    __device__ __forceinline__ static void load(const uint8_t* blk, int u, Raw& raw) {
+        ld_span<8, AL>(blk, raw.hd);
+        ld_span<32, AL>(blk + 8 + 32 * u, raw.q);
+    }
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void dot(const Raw (&raw)[R], int u, const XV& xv,
                                                float (&acc)[R][B]) {
-        uint32_t hd[R][2], q[R][8];
-#pragma unroll
-        for (int r = 0; r < R; ++r) {
-            ld_span<8, AL>(blk[r], hd[r]);
-            ld_span<32, AL>(blk[r] + 8 + 32 * u, q[r]);
-        }
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const lds_f* s16 = xv.xs16 + b * xv.ld16 + 4 * u;
 #pragma unroll
             for (int r = 0; r < R; ++r) {
-                const uint32_t sl = (hd[r][1] >> (8 * u)) & 0xFF;
-                const uint32_t sh = hd[r][0] >> 16;
+                const uint32_t sl = (raw[r].hd[1] >> (8 * u)) & 0xFF;
+                const uint32_t sh = raw[r].hd[0] >> 16;
                 float tot = 0.f;
 #pragma unroll
                 for (int s = 0; s < 2; ++s) {
@@ -314,14 +316,14 @@ template <> struct Unit<T_IQ4_XS> {
                     uint32_t lo[4], hi[4];
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
-                        lo[k] = iq4_lut4(q[r][4 * s + k] & 0x0F0F0F0Fu);
-                        hi[k] = iq4_lut4((q[r][4 * s + k] >> 4) & 0x0F0F0F0Fu);
+                        lo[k] = iq4_lut4(raw[r].q[4 * s + k] & 0x0F0F0F0Fu);
+                        hi[k] = iq4_lut4((raw[r].q[4 * s + k] >> 4) & 0x0F0F0F0Fu);
                     }
                     const float sv = dot_run<4>(lo, xv.ptr(b, 64 * u + 32 * s)) + dot_run<4>(hi, xv.ptr(b, 64 * u + 32 * s + 16));
                     const float xs = s16[2 * s] + s16[2 * s + 1];
                     tot += ((float)(int)ls - 32.f) * (sv - 128.f * xs);
                 }
-                acc[r][b] += half_bits_to_float(hd[r][0]) * tot;
+                acc[r][b] += half_bits_to_float(raw[r].hd[0]) * tot;
             }
         }
     }
@@ -349,21 +351,23 @@ __device__ __forceinline__ uint32_t at_off(const uint32_t (&w)[N], int k, int of
     template <> struct Unit<T> {                                                                     \
         static constexpr int P = 1, PADI = 32;                                                       \
         static constexpr int NB = Small<T>::NB;                                                      \
-        template <int B, int R, bool AL, class XV>                                                   \
-        __device__ __forceinline__ static void run(const uint8_t* const (&blk)[R], int, const XV& xv,  \
+        struct Raw { uint32_t w[(NB + 3) / 4]; };                                                    \
+        template <bool AL>                                                                           \
+        __device__ __forceinline__ static void load(const uint8_t* blk, int, Raw& raw) {             \
+            ld_span<NB, AL>(blk, raw.w);                                                             \
+        }                                                                                            \
+        template <int B, int R, class XV>                                                            \
+        __device__ __forceinline__ static void dot(const Raw (&raw)[R], int, const XV& xv,           \
                                                    float (&acc)[R][B]) {                             \
-            uint32_t w[R][(NB + 3) / 4];                                                             \
-            _Pragma("unroll") for (int r = 0; r < R; ++r) ld_span<NB, AL>(blk[r], w[r]);              \
             _Pragma("unroll") for (int b = 0; b < B; ++b) {                                          \
                 const auto x0 = xv.ptr(b, 0), x16 = xv.ptr(b, 16);                                   \
                 const lds_f* s16 = xv.xs16 + b * xv.ld16;                                            \
                 const float xs = s16[0] + s16[1];                                                    \
                 _Pragma("unroll") for (int r = 0; r < R; ++r)                                        \
-                    acc[r][b] += small_dot<T>(w[r], x0, x16, xs);                                    \
+                    acc[r][b] += small_dot<T>(raw[r].w, x0, x16, xs);                                \
             }                                                                                        \
         }                                                                                            \
     };
-
 
 // Q4_0: d | qs[16]; d * (q - 8).  native.c:281-288
 template <typename PX>
