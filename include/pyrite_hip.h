@@ -98,6 +98,25 @@ int pyrite_dev_matvec_grouped_timed(int type_id, const pyrite_matvec_desc *descs
 int pyrite_dev_dequantize(int type_id, const void *w, size_t w_len, size_t rows, size_t cols,
                           void *out, int out_f64, void *stream);
 
+/* LM head with greedy selection.  logits[b * ldl + r] = fp32 dot product of
+ * row r with x[b] (as pyrite_dev_matvec), and ids[b] = the first index of the
+ * maximum of the reference's fp64 logits for the same x (fp32 values widened
+ * to double), i.e. what pyrite/executor.py:852-875 followed by
+ * Sampler.greedy (pyrite/sampler.py:12-15) returns.  The id is exact: rows
+ * whose fp32 logit, widened by a rigorous rounding-error bound, could still
+ * be the maximum are recomputed on the device in the reference's own fp64
+ * order.  cols <= 65536.  Uses a per-device workspace grown on first use
+ * (call once outside stream capture before capturing). */
+int pyrite_dev_lm_head_argmax(int type_id, const void *w, size_t w_len, size_t rows, size_t cols,
+                              const float *x, size_t ldx, float *logits, size_t ldl, int32_t *ids,
+                              size_t batch, void *stream);
+
+/* RMSNorm: y[b][i] = x[b][i] * (1 / sqrt(sum_j x[b][j]^2 / n + eps)) * weight[i]
+ * (weight NULL = 1), computed in fp64 and rounded to fp32.  Replaces
+ * pyrite/tensor_ops.py:502-506 and pyrite/executor.py:621-624. */
+int pyrite_dev_rms_norm(const float *x, size_t ldx, const float *weight, size_t n, double eps, float *y,
+                        size_t ldy, size_t batch, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

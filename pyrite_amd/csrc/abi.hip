@@ -13,7 +13,7 @@
 
 #include <string>
 
-#include "../../include/pyrite_hip.h"
+#include "pyrite_hip.h"
 #include "dispatch.h"
 
 using namespace pyrite;
@@ -170,6 +170,26 @@ int pyrite_dev_dequantize(int type_id, const void* w, size_t w_len, size_t rows,
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;
     const int rc = dequant_launch(type_id, static_cast<const uint8_t*>(w), w_len, rows, cols, out, out_f64, s);
     if (rc == -4) return fail(-4, "pyrite_dev_dequantize: launch", hipGetLastError());
+    return rc;
+}
+
+int pyrite_dev_lm_head_argmax(int type_id, const void* w, size_t w_len, size_t rows, size_t cols, const float* x,
+                              size_t ldx, float* logits, size_t ldl, int32_t* ids, size_t batch, void* stream) {
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;
+    const int rc = lm_head_launch(type_id, static_cast<const uint8_t*>(w), w_len, rows, cols, x, ldx, logits, ldl,
+                                  reinterpret_cast<int*>(ids), batch, s);
+    if (rc == -4) {
+        if (const char* m = lm_last_error()) return fail(-4, m);
+        return fail(-4, "pyrite_dev_lm_head_argmax: launch", hipGetLastError());
+    }
+    return rc;
+}
+
+int pyrite_dev_rms_norm(const float* x, size_t ldx, const float* weight, size_t n, double eps, float* y, size_t ldy,
+                        size_t batch, void* stream) {
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;
+    const int rc = rms_norm_launch(x, ldx, weight, n, eps, y, ldy, batch, s);
+    if (rc == -4) return fail(-4, "pyrite_dev_rms_norm: launch", hipGetLastError());
     return rc;
 }
 

@@ -80,6 +80,16 @@ int matvec_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t 
 int matvec64_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const double* X,
                     double* Y, hipStream_t stream);
 
+// lmhead.hip: fp32 logits of every row plus ids[b] = first index of the
+// maximum of the reference's fp64 logits, for b < batch.
+int lm_head_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* X, size_t ldx,
+                   float* logits, size_t ldl, int* ids, size_t batch, hipStream_t stream);
+const char* lm_last_error();
+
+// norm.hip: RMSNorm of batch vectors of n floats (Wt may be null: weight 1).
+int rms_norm_launch(const float* X, size_t ldx, const float* Wt, size_t n, double eps, float* Y, size_t ldy,
+                    size_t batch, hipStream_t stream);
+
 // dequant.hip: exact dequantization into fp32 (out_f64 == 0) or fp64.
 int dequant_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, void* out, int out_f64,
                    hipStream_t stream);

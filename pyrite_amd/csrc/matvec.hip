@@ -1,497 +1,21 @@
-// Fused GGML dequantize x matvec for gfx950 (VALU path, batch 1..8).
-//
-// Y[b][row] = sum_c dequant(W)[row][c] * X[b][c] for every row of a verbatim
-// GGUF matrix (rows x row_bytes), fp32 accumulation.  Mirrors the semantics of
-// pyrite_matvec (pyrite/kernels/native.c:518-555) with fp32 instead of fp64
-// arithmetic and a different summation order.
-//
-// Work decomposition: a workgroup is 4 wave64s.  A wave is split into
-// 64/LPR row slots of LPR lanes (LPR = lanes per row, a power of two chosen so
-// a row's units fill it); each slot owns R consecutive rows and its lanes
-// stride over the units of those rows (a unit = one block, or a quarter of a
-// 256-element super-block).  Lanes load whole units with dword-aligned 16-byte
-// loads, decode in registers and accumulate in fp32; the slot then reduces
-// with lane shuffles.  Per-16-column sums of X (needed by formats with a block
-// minimum or code offset) are built once per workgroup in LDS.
-#include <hip/hip_ext.h>
-#include <stdlib.h>
-#include <string.h>
-
-#include <type_traits>
-
-#include "common.h"
-#include "dispatch.h"
-#include "mv_units.h"
+// Fused GGML dequantize x matvec for gfx950: plain fp32 matvec entry points
+// (VALU kernels of mv_kernel.h for batch chunks of 1-2, or any batch when the
+// MFMA path does not apply; MFMA kernels of mx.hip for batch >= 3).
+#include "mv_kernel.h"
 
 namespace pyrite {
-
-// One matrix of a grouped launch.  wg_begin is the first workgroup (blockIdx.x)
-// assigned to this matrix; matrices occupy consecutive workgroup ranges.
-struct MvDesc {
-    const uint8_t* W;
-    unsigned long long row_bytes;
-    const float* X;
-    unsigned long long ldx;
-    float* Y;
-    unsigned long long ldy;
-    int rows;
-    int cols;
-    int lpr_log2;
-    int wg_begin;  // first workgroup of this matrix
-    int wg_count;  // workgroups assigned; each loops over row groups wg, wg + wg_count, ...
-    int pad;
-};
-
-constexpr int kMaxGroup = 16;
-struct MvGroup {
-    int n;
-    MvDesc d[kMaxGroup];
-};
-
-// XL: activations staged in LDS (padded, see XView) instead of read from
-// global memory by every unit; used when B * cols fits the LDS budget.
-template <int T, int B, int R, bool AL, bool XL>
-__device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* smem) {
-    constexpr int BS = Geo<T>::bs, BPB = Geo<T>::bpb;
-    const uint8_t* __restrict__ W = d.W;
-    const float* __restrict__ X = d.X;
-    const int rows = d.rows, cols = d.cols, lpr_log2 = d.lpr_log2;
-    const unsigned long long ldx = d.ldx;
-    const int n16 = cols >> 4;
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int LPR = 1 << lpr_log2, nslot = 64 >> lpr_log2;
-    const int slot = lane >> lpr_log2, li = lane & (LPR - 1);
-    const long long rows_per_wg = 4LL * nslot * R;
-    const long long wave_rows = (long long)nslot * R;
-    const long long stride_rows = (long long)d.wg_count * rows_per_wg;  // rows between row groups of this workgroup
-    long long wrow0 = (wg * 4 + wave) * wave_rows;                        // first row of this wave (wave-uniform)
-    long long row0 = wrow0 + (long long)slot * R;                         // first row of this lane's slot
-
-    float acc[R][B];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int b = 0; b < B; ++b) acc[r][b] = 0.f;
-
-    // reduce the slot's partial sums, store rows row0..row0+R-1, clear acc
-    auto flush = [&](long long r0) {
-        group_sum(acc, lpr_log2);
-        if (li == 0) {
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (r0 + r < rows)
-#pragma unroll
-                    for (int b = 0; b < B; ++b) d.Y[b * d.ldy + r0 + r] = acc[r][b];
-        }
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int b = 0; b < B; ++b) acc[r][b] = 0.f;
-    };
-
-    if constexpr (BS > 1) {
-        // Software pipeline over the lane's (row group, unit) sequence: the
-        // next unit's weights (possibly of the next row group) are loaded
-        // before the current unit is decoded, so every lane keeps two units
-        // of loads in flight.  The unit count per row group is wave-uniform
-        // (KU), which keeps the reduction converged.
-        using Un = Unit<T>;
-        using Raw = typename Un::Raw;
-        constexpr int P = Un::P;
-        static_assert((P & (P - 1)) == 0, "units per block must be a power of two");
-        constexpr int PL = P == 4 ? 2 : 0;
-        constexpr int PADI = Un::PADI;
-        const int U = (cols / BS) * P;
-        const int KU = (U + LPR - 1) >> lpr_log2;
-        // Row pointers (clamped to the last row) of the current and the next row group.
-        auto row_ptrs = [&](long long r0, const uint8_t* (&rp)[R]) {
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const long long rr = (r0 + r < rows) ? r0 + r : (long long)rows - 1;
-                rp[r] = W + rr * d.row_bytes;
-            }
-        };
-        const uint8_t* rp_cur[R];
-        const uint8_t* rp_nxt[R];
-        row_ptrs(row0, rp_cur);
-        row_ptrs(row0 + stride_rows, rp_nxt);
-        // Loads are issued unconditionally (unit index clamped to the row's
-        // last unit, rows clamped to the last row) so that every path through
-        // the loop has the same number of loads in flight and the waits before
-        // a decode cover only the older loads.
-        auto load_item = [&](Raw (&dst)[R], const uint8_t* const (&rp)[R], int u) {
-            const unsigned uu = (unsigned)(u < U ? u : U - 1);
-            const unsigned blk = uu >> PL, part = uu & (P - 1);
-#pragma unroll
-            for (int r = 0; r < R; ++r) Un::template load<AL>(rp[r] + (size_t)blk * BPB, (int)part, dst[r]);
-        };
-        Raw ra[R], rb[R];
-        load_item(ra, rp_cur, li);  // first weights in flight while the activations are staged
-
-        // Per-16-column sums of X (and, with XL, the padded copy of X) in LDS, one pass.
-        lds_f* xs16 = (lds_f*)(smem);  // address-space cast: smem is LDS
-        const int ldxl = cols + (cols / PADI) * 4;
-        lds_f* xl = xs16 + ((B * n16 + 3) & ~3);
-        for (int i = threadIdx.x; i < B * n16; i += blockDim.x) {
-            const int b = i / n16, j = i - b * n16;
-            const float* p = X + b * ldx + 16 * j;
-            const float4 a = ld_x4(p), c = ld_x4(p + 4), e = ld_x4(p + 8), f = ld_x4(p + 12);
-            xs16[i] = (((a.x + a.y) + (a.z + a.w)) + ((c.x + c.y) + (c.z + c.w))) +
-                      (((e.x + e.y) + (e.z + e.w)) + ((f.x + f.y) + (f.z + f.w)));
-            if constexpr (XL) {
-                // 16 columns never straddle a pad (PADI is a multiple of 16)
-                lds_f* q = xl + b * ldxl + 16 * j + (16 * j / PADI) * 4;
-                st_x4(q, a); st_x4(q + 4, c); st_x4(q + 8, e); st_x4(q + 12, f);
-            }
-        }
-        __syncthreads();
-        if (wrow0 >= rows) return;
-
-        XView<XL, PADI> xv;
-        xv.ldx = XL ? (size_t)ldxl : (size_t)ldx;
-        xv.ld16 = n16;
-        auto dot_item = [&](const Raw (&src)[R], int u) {
-            const unsigned blk = (unsigned)u >> PL, part = (unsigned)u & (P - 1);
-            if constexpr (XL) xv.x = xl + blk * BS + (blk * BS / PADI) * 4;
-            else xv.x = X + (size_t)blk * BS;
-            xv.xs16 = xs16 + blk * (BS / 16);
-            Un::template dot<B, R>(src, (int)part, xv, acc);
-        };
-        int k = 0;
-        // one pipeline step: decode cur (unit k), with unit k+1 loaded into nxt; true when done
-        auto step = [&](Raw (&cur)[R], Raw (&nxt)[R]) -> bool {
-            const int u = li + (k << lpr_log2);
-            const bool adv = (k + 1 == KU);
-            const int un = adv ? li : u + LPR;
-            const uint8_t* rpl[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) rpl[r] = adv ? rp_nxt[r] : rp_cur[r];
-            load_item(nxt, rpl, un);
-            if (u < U) dot_item(cur, u);
-            if (adv) {
-                flush(row0);
-                wrow0 += stride_rows;
-                if (wrow0 >= rows) return true;
-                row0 += stride_rows;
-#pragma unroll
-                for (int r = 0; r < R; ++r) rp_cur[r] = rp_nxt[r];
-                row_ptrs(row0 + stride_rows, rp_nxt);
-                k = 0;
-            } else {
-                ++k;
-            }
-            return false;
-        };
-        for (;;) {
-            if (step(ra, rb)) break;
-            if (step(rb, ra)) break;
-        }
-    } else {
-        if (wrow0 >= rows) return;
-        for (;;) {
-            const int U = (cols + 3) >> 2;
-            const uint8_t* rp[R];
-#pragma unroll
-            for (int r = 0; r < R; ++r) {
-                const long long rr = (row0 + r < rows) ? row0 + r : (long long)rows - 1;
-                rp[r] = W + rr * d.row_bytes;
-            }
-            for (int u = li; u < U; u += LPR) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int col = 4 * u + e;
-                    if (col < cols) {
-#pragma unroll
-                        for (int r = 0; r < R; ++r) {
-                            const float w = plain_elem<T>(rp[r] + (size_t)col * BPB);
-#pragma unroll
-                            for (int b = 0; b < B; ++b) acc[r][b] = fmaf(w, X[b * ldx + col], acc[r][b]);
-                        }
-                    }
-                }
-            }
-            flush(row0);
-            wrow0 += stride_rows;
-            if (wrow0 >= rows) break;
-            row0 += stride_rows;
-        }
-    }
-}
-
-template <int T, int B, int R, bool AL, bool XL>
-__global__ __launch_bounds__(256) void mv_kernel(const MvGroup g) {
-    extern __shared__ float smem[];
-    int i = 0;
-    while (i + 1 < g.n && (int)blockIdx.x >= g.d[i + 1].wg_begin) ++i;
-    mv_body<T, B, R, AL, XL>(g.d[i], (long long)blockIdx.x - g.d[i].wg_begin, smem);
-}
-
-// ---------------------------------------------------------------- launcher
-
-static int log2_ceil(long long v) {
-    int l = 0;
-    while ((1LL << l) < v) ++l;
-    return l;
-}
-
-template <int T>
-static long long units_per_row(int cols) {
-    constexpr int BS = Geo<T>::bs;
-    if constexpr (BS > 1) return (long long)(cols / BS) * Unit<T>::P;
-    else return (cols + 3) / 4;
-}
-
-// A launch uses at most as many workgroups as the device holds at once
-// (persistent workgroups): each loops over row groups, so the per-workgroup
-// prologue (activations and their 16-column sums staged in LDS) is paid once
-// per resident workgroup instead of once per row group.
-struct DevInfo {
-    int cus;
-    size_t lds_per_cu;
-};
-static const DevInfo& dev_info() {
-    static const DevInfo info = [] {
-        DevInfo i{256, 160 * 1024};
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess) {
-            if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) i.cus = v;
-            if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) == hipSuccess && v > 0)
-                i.lds_per_cu = (size_t)v;
-        }
-        return i;
-    }();
-    return info;
-}
-
-// Workgroups of one kernel instance resident per CU, from its register use.
-template <int T, int B, int R, bool AL, bool XL>
-static int wgs_per_cu_regs() {
-    static const int n = [] {
-        int v = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, mv_kernel<T, B, R, AL, XL>, 256, 0) != hipSuccess || v < 1)
-            v = 1;
-        return v;
-    }();
-    return n;
-}
-
-// Optional tuning override "R,KU" (rows per slot, units per lane) from
-// PYRITE_MATVEC_SHAPE; 0 means "choose".
-struct ShapeOverride {
-    int r = 0, ku = 0;
-};
-static const ShapeOverride& shape_override() {
-    static const ShapeOverride o = [] {
-        ShapeOverride v;
-        const char* e = getenv("PYRITE_MATVEC_SHAPE");
-        if (e) {
-            v.r = atoi(e);
-            const char* c = strchr(e, ',');
-            if (c) v.ku = atoi(c + 1);
-        }
-        return v;
-    }();
-    return o;
-}
-
-// Slot geometry for one matrix: the largest units-per-lane KU (<= 8) whose
-// slots still give at least `target` waves, so the per-row-group cost (lane
-// reduction, row pointers, store) is spread over several units without
-// leaving resident waves idle.  Returns lpr_log2 and the waves it needs.
-static int plan_lpr(long long U, long long rows, int R, long long target, long long* waves_out) {
-    int best = -1;
-    long long best_w = 0;
-    const int forced = shape_override().ku;
-    for (int ku = 1; ku <= 8; ku *= 2) {
-        if (forced && ku != forced) continue;
-        const long long per_lane = (U + ku - 1) / ku;
-        const int lg = log2_ceil(per_lane < 64 ? per_lane : 64);
-        const long long rows_per_wave = (long long)(64 >> lg) * R;
-        const long long w = (rows + rows_per_wave - 1) / rows_per_wave;
-        if (best < 0 || forced || w >= target) { best = lg; best_w = w; }
-        if (w < target) break;
-    }
-    *waves_out = best_w;
-    return best;
-}
-
-template <int T, int B, int R, bool AL, bool XL>
-static long long resident_wgs(size_t lds) {
-    const DevInfo& di = dev_info();
-    long long per_cu = wgs_per_cu_regs<T, B, R, AL, XL>();
-    if (lds > 0 && (long long)(di.lds_per_cu / lds) < per_cu) per_cu = (long long)(di.lds_per_cu / lds);
-    if (per_cu < 1) per_cu = 1;
-    return per_cu * di.cus;
-}
-
-// LDS bytes of a launch: per-16-column sums, plus the padded activations when staged.
-template <int T, int B>
-static size_t lds_bytes(int max_cols, bool xl) {
-    if constexpr (Geo<T>::bs == 1) {
-        return 0;
-    } else {
-        size_t n = (size_t)B * (max_cols / 16) * sizeof(float);
-        if (xl) {
-            constexpr int PADI = Unit<T>::PADI;
-            n = ((n / sizeof(float) + 3) & ~size_t(3)) * sizeof(float) +
-                (size_t)B * (max_cols + (max_cols / PADI) * 4) * sizeof(float);
-        }
-        return n;
-    }
-}
-template <int T, int B>
-static bool use_xl(int max_cols) {
-    return Geo<T>::bs > 1 && B <= 2 && lds_bytes<T, B>(max_cols, true) <= 65536;
-}
-
-// Slot shape of one matrix (rows per slot R, lanes per row), a function of
-// the matrix and the device only, so a matrix gives bit-identical results
-// whether it is launched alone or in a group.  B == 1 uses two rows per slot
-// (every activation read serves both) unless that leaves resident waves idle.
-struct MatShape {
-    int R;
-    int lpr_log2;
-};
-template <int T, int B, bool AL>
-static MatShape mat_shape(int rows, int cols) {
-    const long long U = units_per_row<T>(cols);
-    const bool xl = use_xl<T, B>(cols);
-    const size_t lds = lds_bytes<T, B>(cols, xl);
-    int R = 1;
-    if constexpr (B == 1) {
-        const int forced = shape_override().r;
-        if (forced) {
-            R = forced == 2 ? 2 : 1;
-        } else {
-            long long w = 0;
-            plan_lpr(U, rows, 2, 1LL << 40, &w);  // waves at one unit per lane
-            const long long target = 4 * (xl ? resident_wgs<T, B, 2, AL, true>(lds) : resident_wgs<T, B, 2, AL, false>(lds));
-            R = (w >= target) ? 2 : 1;
-        }
-    }
-    long long target = 4 * (xl ? resident_wgs<T, B, 1, AL, true>(lds) : resident_wgs<T, B, 1, AL, false>(lds));
-    if constexpr (B == 1) {
-        if (R == 2) target = 4 * (xl ? resident_wgs<T, B, 2, AL, true>(lds) : resident_wgs<T, B, 2, AL, false>(lds));
-    }
-    long long w = 0;
-    return MatShape{R, plan_lpr(U, rows, R, target, &w)};
-}
-
-// Fill wg_begin / wg_count (lpr_log2 is already set) and return the total
-// number of workgroups (at most cap).  Each matrix gets workgroups in
-// proportion to its weight bytes, never more than it has row groups.
-static long long plan_group(MvGroup& g, int R, long long cap) {
-    double total_bytes = 0;
-    for (int i = 0; i < g.n; ++i) total_bytes += (double)g.d[i].rows * (double)g.d[i].row_bytes;
-    long long wg = 0;
-    for (int i = 0; i < g.n; ++i) {
-        const double frac = ((double)g.d[i].rows * (double)g.d[i].row_bytes) / (total_bytes > 0 ? total_bytes : 1.0);
-        long long share = (long long)((double)cap * frac);
-        if (share < 1) share = 1;
-        const long long rows_per_wg = 4LL * (64 >> g.d[i].lpr_log2) * R;
-        const long long need = (g.d[i].rows + rows_per_wg - 1) / rows_per_wg;
-        const long long cnt = need < share ? need : share;
-        g.d[i].wg_begin = (int)wg;
-        g.d[i].wg_count = (int)cnt;
-        wg += cnt;
-    }
-    return wg;
-}
-
-// Optional start/stop events are recorded by the launch itself
-// (hipExtLaunchKernelGGL), so they bracket the kernel's execution on the GPU.
-struct LaunchEvents {
-    hipEvent_t start = nullptr;
-    hipEvent_t stop = nullptr;
-};
-
-template <int T, int B, int R, bool AL, bool XL>
-static hipError_t launch_group_r(MvGroup g, size_t lds, hipStream_t stream, LaunchEvents ev) {
-    const long long wgs = plan_group(g, R, resident_wgs<T, B, R, AL, XL>(lds));
-    if (wgs <= 0 || wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
-    if (ev.start || ev.stop)
-        hipExtLaunchKernelGGL((mv_kernel<T, B, R, AL, XL>), dim3((unsigned)wgs), dim3(256), (uint32_t)lds, stream,
-                              ev.start, ev.stop, 0, g);
-    else
-        hipLaunchKernelGGL((mv_kernel<T, B, R, AL, XL>), dim3((unsigned)wgs), dim3(256), lds, stream, g);
-    return hipGetLastError();
-}
-
-template <int T, int B, int R, bool AL>
-static hipError_t launch_group_rx(const MvGroup& g, hipStream_t stream, LaunchEvents ev) {
-    int max_cols = 0;
-    for (int i = 0; i < g.n; ++i) max_cols = g.d[i].cols > max_cols ? g.d[i].cols : max_cols;
-    if (use_xl<T, B>(max_cols))
-        return launch_group_r<T, B, R, AL, true>(g, lds_bytes<T, B>(max_cols, true), stream, ev);
-    return launch_group_r<T, B, R, AL, false>(g, lds_bytes<T, B>(max_cols, false), stream, ev);
-}
-
-// Split the group by rows-per-slot (one launch per R present).
-template <int T, int B, bool AL>
-static hipError_t launch_group(const MvGroup& g, hipStream_t stream, LaunchEvents ev) {
-    MvGroup by_r[2];
-    by_r[0].n = by_r[1].n = 0;
-    for (int i = 0; i < g.n; ++i) {
-        const MatShape sh = mat_shape<T, B, AL>(g.d[i].rows, g.d[i].cols);
-        MvDesc d = g.d[i];
-        d.lpr_log2 = sh.lpr_log2;
-        MvGroup& dst = by_r[sh.R - 1];
-        dst.d[dst.n++] = d;
-    }
-    const int first = by_r[0].n ? 0 : 1, last = by_r[1].n ? 1 : 0;
-    for (int k = first; k <= last; ++k) {
-        if (by_r[k].n == 0) continue;
-        LaunchEvents e;
-        if (k == first) e.start = ev.start;
-        if (k == last) e.stop = ev.stop;
-        hipError_t err = hipSuccess;
-        if constexpr (B == 1) {
-            err = k ? launch_group_rx<T, B, 2, AL>(by_r[k], stream, e) : launch_group_rx<T, B, 1, AL>(by_r[k], stream, e);
-        } else {
-            err = launch_group_rx<T, B, 1, AL>(by_r[k], stream, e);
-        }
-        if (err != hipSuccess) return err;
-    }
-    return hipSuccess;
-}
-
-template <int T, bool AL>
-static hipError_t launch_type(int batch, const MvGroup& g, hipStream_t s, LaunchEvents ev) {
-    switch (batch) {
-    case 1: return launch_group<T, 1, AL>(g, s, ev);
-    case 2: return launch_group<T, 2, AL>(g, s, ev);
-    case 4: return launch_group<T, 4, AL>(g, s, ev);
-    case 8: return launch_group<T, 8, AL>(g, s, ev);
-    default: return hipErrorInvalidValue;
-    }
-}
 
 int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, hipStream_t stream,
                         hipEvent_t start, hipEvent_t stop) {
     const TypeGeo g = type_geo(type);
-    if (!g.valid) return -1;
-    if (n == 0 || batch == 0) return -2;
-    const bool quant = g.bs > 1;
-    bool al = (g.bpb % 4 == 0);
+    bool al = false;
     size_t max_cols = 0;
-    for (size_t i = 0; i < n; ++i) {
-        const MatvecArgs& m = mats[i];
-        if (m.rows == 0 || m.cols == 0 || m.cols % g.bs != 0) return -2;
-        if (m.rows > 0x7FFFFFFF || m.cols > 0x7FFFFFFF) return -2;
-        const size_t row_bytes = m.cols / g.bs * g.bpb;
-        if (m.w_len != m.rows * row_bytes) return -3;
-        if (!m.w || !m.x || !m.y || m.ldx < m.cols || m.ldy < m.rows) return -3;
-        if (quant && ((reinterpret_cast<uintptr_t>(m.x) & 15u) || (m.ldx & 3u))) return -3;
-        if (!quant && (reinterpret_cast<uintptr_t>(m.w) % g.bpb)) return -3;
-        if (reinterpret_cast<uintptr_t>(m.w) & 3u) al = false;
-        if (m.cols > max_cols) max_cols = m.cols;
-    }
+    if (const int rc = validate_group(g, mats, n, batch, &al, &max_cols)) return rc;
     static const int forced = [] {
         const char* v = getenv("PYRITE_MATVEC_PATH");  // "valu" forces the VALU kernels
         return (v && v[0] == 'v') ? 1 : 0;
     }();
-    if (quant && !forced && batch >= 3 && mx_type_supported(type)) {
+    if (g.bs > 1 && !forced && batch >= 3 && mx_type_supported(type)) {
         for (size_t done = 0; done < batch; done += 8) {
             const size_t c = batch - done < 8 ? batch - done : 8;
             const int rc = mx_group_launch(type, mats, n, c, done, al, stream, done == 0 ? start : nullptr,
@@ -500,49 +24,7 @@ int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch
         }
         return 0;
     }
-    size_t done = 0;
-    while (done < batch) {
-        // largest instantiated batch chunk whose per-16-column x sums fit 64 KiB of LDS
-        int c = 0;
-        for (int cand : {8, 4, 2, 1}) {
-            if ((size_t)cand > batch - done) continue;
-            if (!quant || (size_t)cand * (max_cols / 16) * sizeof(float) <= 65536) { c = cand; break; }
-        }
-        if (c == 0) return -2;
-        for (size_t base = 0; base < n; base += kMaxGroup) {
-            LaunchEvents ev;
-            if (done == 0 && base == 0) ev.start = start;
-            if (done + c >= batch && base + kMaxGroup >= n) ev.stop = stop;
-            MvGroup grp;
-            grp.n = (int)((n - base) < (size_t)kMaxGroup ? (n - base) : (size_t)kMaxGroup);
-            for (int i = 0; i < grp.n; ++i) {
-                const MatvecArgs& m = mats[base + i];
-                MvDesc& dd = grp.d[i];
-                dd.W = static_cast<const uint8_t*>(m.w);
-                dd.row_bytes = m.cols / g.bs * g.bpb;
-                dd.X = m.x + done * m.ldx;
-                dd.ldx = m.ldx;
-                dd.Y = m.y + done * m.ldy;
-                dd.ldy = m.ldy;
-                dd.rows = (int)m.rows;
-                dd.cols = (int)m.cols;
-            }
-            hipError_t e = hipSuccess;
-#define PYRITE_CASE(T)                                                                       \
-    case T:                                                                                \
-        e = al ? launch_type<T, (Geo<T>::bpb % 4 == 0)>(c, grp, stream, ev)                \
-               : launch_type<T, false>(c, grp, stream, ev);                                \
-        break;
-            switch (type) {
-                PYRITE_FOR_EACH_TYPE(PYRITE_CASE)
-            default: return -1;
-            }
-#undef PYRITE_CASE
-            if (e != hipSuccess) return -4;
-        }
-        done += c;
-    }
-    return 0;
+    return valu_group_launch<false>(type, g, al, mats, nullptr, n, batch, max_cols, stream, start, stop);
 }
 
 int matvec_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* X, size_t ldx,

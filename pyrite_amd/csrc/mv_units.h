@@ -9,6 +9,13 @@
 // q_i are converted with v_cvt_f32_ubyte{0..3}; sum_i x_i over every 16
 // columns is precomputed per workgroup in LDS (xs16).  Element order inside a
 // unit follows each block layout (pyrite/kernels/native.c:129-437).
+//
+// bound() accumulates, per row and batch vector, an upper bound of the sum of
+// the magnitudes of every product dot() forms for the unit (codes, offsets and
+// minima counted separately, as dot() multiplies them), using per-16-column
+// sums of |x|.  The fp32 rounding error of the matvec is at most
+// gamma_depth times this sum; the LM-head argmax uses it to decide which rows
+// can still hold the maximum of the exact logits.
 #pragma once
 
 #include <type_traits>
@@ -41,7 +48,8 @@ struct XView {
     P x;                // activations of column 0 of this block, batch 0
     size_t ldx;         // floats between batch rows
     const lds_f* xs16;  // LDS: sum of each 16 columns, batch 0, from column 0 of this block
-    int ld16;           // floats between batch rows in xs16
+    const lds_f* xa16;  // LDS: sum of |x| over each 16 columns (same indexing; bound pass only)
+    int ld16;           // floats between batch rows in xs16 / xa16
     __device__ __forceinline__ P ptr(int b, int off) const {
         if constexpr (XL) return x + b * ldx + off + (off / PADI) * 4;
         else return x + b * ldx + off;
@@ -109,6 +117,22 @@ template <> struct Unit<T_Q4_K> {
             }
         }
     }
+    // leaves: d*sc*q*x (q <= 15) and dmin*m*x
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void bound(const Raw (&raw)[R], int c, const XV& xv, float (&bacc)[R][B]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float sc0, m0, sc1, m1;
+            k4_pair_regs(raw[r].hd[1], raw[r].hd[2], raw[r].hd[3], c, sc0, m0, sc1, m1);
+            const float d = fabsf(half_bits_to_float(raw[r].hd[0])), dm = fabsf(half_bits_to_float(raw[r].hd[0] >> 16));
+            const float k0 = d * sc0 * 15.f + dm * m0, k1 = d * sc1 * 15.f + dm * m1;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const lds_f* a = xv.xa16 + b * xv.ld16 + 4 * c;
+                bacc[r][b] += k0 * (a[0] + a[1]) + k1 * (a[2] + a[3]);
+            }
+        }
+    }
 };
 
 // ------------------------------------------------------------------ Q5_K
@@ -144,6 +168,22 @@ template <> struct Unit<T_Q5_K> {
                 k4_pair_regs(raw[r].hd[1], raw[r].hd[2], raw[r].hd[3], c, sc0, m0, sc1, m1);
                 const float d = half_bits_to_float(raw[r].hd[0]), dmin = half_bits_to_float(raw[r].hd[0] >> 16);
                 acc[r][b] += d * (sc0 * slo + sc1 * shi) - dmin * (m0 * xlo + m1 * xhi);
+            }
+        }
+    }
+    // leaves: d*sc*q*x (q <= 31) and dmin*m*x
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void bound(const Raw (&raw)[R], int c, const XV& xv, float (&bacc)[R][B]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float sc0, m0, sc1, m1;
+            k4_pair_regs(raw[r].hd[1], raw[r].hd[2], raw[r].hd[3], c, sc0, m0, sc1, m1);
+            const float d = fabsf(half_bits_to_float(raw[r].hd[0])), dm = fabsf(half_bits_to_float(raw[r].hd[0] >> 16));
+            const float k0 = d * sc0 * 31.f + dm * m0, k1 = d * sc1 * 31.f + dm * m1;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const lds_f* a = xv.xa16 + b * xv.ld16 + 4 * c;
+                bacc[r][b] += k0 * (a[0] + a[1]) + k1 * (a[2] + a[3]);
             }
         }
     }
@@ -194,6 +234,26 @@ template <> struct Unit<T_Q6_K> {
             }
         }
     }
+    // leaves: d*sc*q*x (q <= 63) and d*sc*32*x
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void bound(const Raw (&raw)[R], int u, const XV& xv, float (&bacc)[R][B]) {
+        const int h = u >> 1, rr = u & 1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float d = fabsf(half_bits_to_float(raw[r].D[0])) * 95.f;
+            float k[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t sw = raw[r].S[g >> 1] >> (8 * (rr + 2 * (g & 1)));
+                k[g] = d * fabsf((float)(int)(int8_t)(sw & 0xFF));
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const lds_f* a = xv.xa16 + b * xv.ld16 + 8 * h + rr;
+                bacc[r][b] += k[0] * a[0] + k[1] * a[2] + k[2] * a[4] + k[3] * a[6];
+            }
+        }
+    }
 };
 
 // ------------------------------------------------------------------ Q2_K
@@ -232,6 +292,26 @@ template <> struct Unit<T_Q2_K> {
                     tm += (float)(sb >> 4) * s16[2 * g];
                 }
                 acc[r][b] += half_bits_to_float(raw[r].D[0]) * ts - half_bits_to_float(raw[r].D[0] >> 16) * tm;
+            }
+        }
+    }
+    // leaves: d*sc*q*x (q <= 3) and dmin*m*x
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void bound(const Raw (&raw)[R], int u, const XV& xv, float (&bacc)[R][B]) {
+        const int h = u >> 1, rr = u & 1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float d = fabsf(half_bits_to_float(raw[r].D[0])) * 3.f, dm = fabsf(half_bits_to_float(raw[r].D[0] >> 16));
+            float k[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t sb = (raw[r].S[g >> 1] >> (8 * (rr + 2 * (g & 1)))) & 0xFF;
+                k[g] = d * (float)(sb & 15) + dm * (float)(sb >> 4);
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const lds_f* a = xv.xa16 + b * xv.ld16 + 8 * h + rr;
+                bacc[r][b] += k[0] * a[0] + k[1] * a[2] + k[2] * a[4] + k[3] * a[6];
             }
         }
     }
@@ -284,6 +364,29 @@ template <> struct Unit<T_Q3_K> {
             }
         }
     }
+    // leaves: d*sc*c*x (c <= 7) and d*sc*4*x
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void bound(const Raw (&raw)[R], int u, const XV& xv, float (&bacc)[R][B]) {
+        const int h = u >> 1, rr = u & 1;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float d = fabsf(half_bits_to_float(raw[r].D[0])) * 11.f;
+            float k[4];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t lb = (raw[r].S[g >> 1] >> (8 * (rr + 2 * (g & 1)))) & 0xFF;
+                const uint32_t low4 = h ? (lb >> 4) : (lb & 15);
+                const uint32_t hb = (raw[r].S[2] >> (8 * ((2 * g + rr) & 3))) & 0xFF;
+                const uint32_t hi2 = (hb >> (2 * (2 * h + (g >> 1)))) & 3;
+                k[g] = d * fabsf((float)(int)(low4 | (hi2 << 4)) - 32.f);
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const lds_f* a = xv.xa16 + b * xv.ld16 + 8 * h + rr;
+                bacc[r][b] += k[0] * a[0] + k[1] * a[2] + k[2] * a[4] + k[3] * a[6];
+            }
+        }
+    }
 };
 
 // ------------------------------------------------------------------ IQ4_XS
@@ -327,6 +430,28 @@ template <> struct Unit<T_IQ4_XS> {
             }
         }
     }
+    // leaves: d*(ls-32)*(K+128)*x (K+128 <= 241) and d*(ls-32)*128*x
+    template <int B, int R, class XV>
+    __device__ __forceinline__ static void bound(const Raw (&raw)[R], int u, const XV& xv, float (&bacc)[R][B]) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const uint32_t sl = (raw[r].hd[1] >> (8 * u)) & 0xFF;
+            const uint32_t sh = raw[r].hd[0] >> 16;
+            const float d = fabsf(half_bits_to_float(raw[r].hd[0])) * 369.f;
+            float k[2];
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2) {
+                const int ib = 2 * u + s2;
+                const uint32_t ls = ((sl >> (4 * s2)) & 15) | (((sh >> (2 * ib)) & 3u) << 4);
+                k[s2] = d * fabsf((float)(int)ls - 32.f);
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const lds_f* a = xv.xa16 + b * xv.ld16 + 4 * u;
+                bacc[r][b] += k[0] * (a[0] + a[1]) + k[1] * (a[2] + a[3]);
+            }
+        }
+    }
 };
 
 // ------------------------------------------------------------------ 32-element blocks
@@ -365,6 +490,17 @@ __device__ __forceinline__ uint32_t at_off(const uint32_t (&w)[N], int k, int of
                 const float xs = s16[0] + s16[1];                                                    \
                 _Pragma("unroll") for (int r = 0; r < R; ++r)                                        \
                     acc[r][b] += small_dot<T>(raw[r].w, x0, x16, xs);                                \
+            }                                                                                        \
+        }                                                                                            \
+        template <int B, int R, class XV>                                                            \
+        __device__ __forceinline__ static void bound(const Raw (&raw)[R], int, const XV& xv,         \
+                                                     float (&bacc)[R][B]) {                          \
+            _Pragma("unroll") for (int r = 0; r < R; ++r) {                                          \
+                const float k = small_coef<T>(raw[r].w);                                             \
+                _Pragma("unroll") for (int b = 0; b < B; ++b) {                                      \
+                    const lds_f* a = xv.xa16 + b * xv.ld16;                                          \
+                    bacc[r][b] += k * (a[0] + a[1]);                                                 \
+                }                                                                                    \
             }                                                                                        \
         }                                                                                            \
     };
@@ -452,6 +588,20 @@ __device__ __forceinline__ float small_dot_T_Q8_1(const uint32_t (&w)[9], PX x, 
     for (int k = 0; k < 8; ++k) c[k] = w[1 + k] ^ 0x80808080u;
     const float s = dot_run<8>(c, x);
     return half_bits_to_float(w[0]) * (s - 128.f * xs);
+}
+
+// Magnitude coefficient of a 32-element block for bound(): every product the
+// block's small_dot forms for column i is at most coef * |x_i|.
+template <int T, int N>
+__device__ __forceinline__ float small_coef(const uint32_t (&w)[N]) {
+    const float d = fabsf(half_bits_to_float(w[0]));
+    if constexpr (T == T_Q4_0) return d * 23.f;                  // q <= 15, offset 8
+    if constexpr (T == T_IQ4_NL) return d * 369.f;               // K + 128 <= 241, offset 128
+    if constexpr (T == T_Q4_1) return d * 15.f + fabsf(half_bits_to_float(w[0] >> 16));
+    if constexpr (T == T_Q5_0) return d * 47.f;                  // q <= 31, offset 16
+    if constexpr (T == T_Q5_1) return d * 31.f + fabsf(half_bits_to_float(w[0] >> 16));
+    if constexpr (T == T_Q8_0 || T == T_Q8_1) return d * 383.f;  // q + 128 <= 255, offset 128
+    return 0.f;
 }
 
 template <int T, int N, typename PX>

@@ -23,6 +23,11 @@ def upload(payload, device: str | torch.device = "cuda") -> torch.Tensor:
     return host.to(device=device, dtype=torch.uint8).contiguous()
 
 
+def _ld(t: torch.Tensor) -> int:
+    """Leading dimension of a [batch, n] tensor (size-1 batches may carry any stride)."""
+    return t.stride(0) if t.shape[0] > 1 else t.shape[1]
+
+
 def _check_weights(type_id: int, w: torch.Tensor, rows: int, cols: int) -> None:
     t = spec(type_id)
     if w.dtype != torch.uint8 or not w.is_cuda or not w.is_contiguous():
@@ -43,8 +48,8 @@ def matvec(type_id: int, w: torch.Tensor, x: torch.Tensor, rows: int, cols: int,
     if out is None:
         out = torch.empty(batch, rows, dtype=torch.float32, device=w.device)
     lib = _lib.load()
-    code = lib.pyrite_dev_matvec(type_id, w.data_ptr(), w.numel(), rows, cols, x2.data_ptr(), x2.stride(0),
-                                 out.data_ptr(), out.stride(0), batch, _stream_ptr(w.device))
+    code = lib.pyrite_dev_matvec(type_id, w.data_ptr(), w.numel(), rows, cols, x2.data_ptr(), _ld(x2),
+                                 out.data_ptr(), _ld(out), batch, _stream_ptr(w.device))
     _lib.check(code, "pyrite_dev_matvec")
     return out.reshape(rows) if squeeze else out
 
@@ -61,3 +66,43 @@ def dequantize(type_id: int, w: torch.Tensor, rows: int, cols: int,
                                      int(dtype == torch.float64), _stream_ptr(w.device))
     _lib.check(code, "pyrite_dev_dequantize")
     return out
+
+
+def lm_head_argmax(type_id: int, w: torch.Tensor, x: torch.Tensor, rows: int, cols: int,
+                   logits: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """LM head: fp32 logits and the exact greedy token per vector.
+
+    ``x`` is [cols] or [batch, cols] fp32.  Returns (logits [batch, rows] fp32,
+    ids [batch] int32); ids equal the first index of the maximum of the
+    reference's fp64 logits (pyrite/executor.py:852-875, pyrite/sampler.py:12-15).
+    """
+    _check_weights(type_id, w, rows, cols)
+    x2 = x.reshape(1, -1) if x.dim() == 1 else x
+    if x2.dtype != torch.float32 or x2.shape[1] != cols or x2.stride(1) != 1:
+        raise ValueError("x must be fp32 [batch, cols] with contiguous rows")
+    batch = x2.shape[0]
+    if logits is None:
+        logits = torch.empty(batch, rows, dtype=torch.float32, device=w.device)
+    ids = torch.empty(batch, dtype=torch.int32, device=w.device)
+    lib = _lib.load()
+    code = lib.pyrite_dev_lm_head_argmax(type_id, w.data_ptr(), w.numel(), rows, cols, x2.data_ptr(),
+                                         _ld(x2), logits.data_ptr(), _ld(logits), ids.data_ptr(),
+                                         batch, _stream_ptr(w.device))
+    _lib.check(code, "pyrite_dev_lm_head_argmax")
+    return logits, ids
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm over the last dim of fp32 x (pyrite/tensor_ops.py:502-506), fp64 inside."""
+    x2 = x.reshape(1, -1) if x.dim() == 1 else x
+    if x2.dtype != torch.float32 or not x2.is_cuda or x2.stride(1) != 1:
+        raise ValueError("x must be an fp32 CUDA tensor with contiguous rows")
+    n = x2.shape[1]
+    if weight is not None and (weight.dtype != torch.float32 or weight.numel() != n or not weight.is_contiguous()):
+        raise ValueError("weight must be a contiguous fp32 tensor of x's last dim")
+    y = torch.empty_like(x2)
+    lib = _lib.load()
+    code = lib.pyrite_dev_rms_norm(x2.data_ptr(), _ld(x2), weight.data_ptr() if weight is not None else None,
+                                   n, float(eps), y.data_ptr(), _ld(y), x2.shape[0], _stream_ptr(x2.device))
+    _lib.check(code, "pyrite_dev_rms_norm")
+    return y.reshape(x.shape)
