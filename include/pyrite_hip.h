@@ -111,6 +111,43 @@ int pyrite_dev_lm_head_argmax(int type_id, const void *w, size_t w_len, size_t r
                               const float *x, size_t ldx, float *logits, size_t ldl, int32_t *ids,
                               size_t batch, void *stream);
 
+/* One Qwen3-MoE FFN layer.  Tensors are GGUF bytes in device memory: the
+ * router [n_experts][hidden] (ffn_gate_inp), and the stacked expert tensors
+ * gate and up [n_experts][inter][hidden] and down [n_experts][hidden][inter]
+ * (expert e = contiguous byte slice e, pyrite/qwen3_moe.py:364-398). */
+typedef struct pyrite_moe_layer {
+    int router_type;
+    const void *router;
+    size_t router_len;
+    int gate_type;
+    const void *gate;
+    size_t gate_len;
+    int up_type;
+    const void *up;
+    size_t up_len;
+    int down_type;
+    const void *down;
+    size_t down_len;
+    size_t n_experts;
+    size_t hidden;
+    size_t inter;
+    size_t k;              /* experts per token (num_experts_per_tok) */
+    int norm_topk_prob;    /* renormalise the k weights when their sum is positive */
+    double scale;          /* expert_weights_scale */
+} pyrite_moe_layer;
+
+/* out[b * ldo + i] = the layer's output for token x[b] (pyrite/executor.py:757-793
+ * with _expert, :672-683): router logits, softmax, experts ranked by (-p, e),
+ * top k, weights (renormalised / scaled), SwiGLU experts, weighted sum in rank
+ * order.  ids[b * k + s] (device int32, may be NULL) receives the chosen
+ * experts in rank order, identical to the reference's; weights (device fp32,
+ * may be NULL) their weights.  The expert ids stay on the device and drive
+ * the expert kernels directly.  n_experts <= 1024, k <= 32, batch <= 4096.
+ * Uses a per-device workspace grown on first use (call once outside stream
+ * capture before capturing). */
+int pyrite_dev_moe_ffn(const pyrite_moe_layer *layer, const float *x, size_t ldx, float *out, size_t ldo,
+                       int32_t *ids, float *weights, size_t batch, void *stream);
+
 /* RMSNorm: y[b][i] = x[b][i] * (1 / sqrt(sum_j x[b][j]^2 / n + eps)) * weight[i]
  * (weight NULL = 1), computed in fp64 and rounded to fp32.  Replaces
  * pyrite/tensor_ops.py:502-506 and pyrite/executor.py:621-624. */

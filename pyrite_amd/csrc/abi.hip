@@ -185,6 +185,20 @@ int pyrite_dev_lm_head_argmax(int type_id, const void* w, size_t w_len, size_t r
     return rc;
 }
 
+int pyrite_dev_moe_ffn(const pyrite_moe_layer* layer, const float* x, size_t ldx, float* out, size_t ldo,
+                       int32_t* ids, float* weights, size_t batch, void* stream) {
+    static_assert(sizeof(pyrite_moe_layer) == sizeof(MoeLayer), "MoE layer layout");
+    if (layer == NULL) return -3;
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;
+    const int rc = moe_ffn_launch(*reinterpret_cast<const MoeLayer*>(layer), x, ldx, out, ldo,
+                                  reinterpret_cast<int*>(ids), weights, batch, s);
+    if (rc == -4) {
+        if (const char* m = moe_last_error()) return fail(-4, m);
+        return fail(-4, "pyrite_dev_moe_ffn: launch", hipGetLastError());
+    }
+    return rc;
+}
+
 int pyrite_dev_rms_norm(const float* x, size_t ldx, const float* weight, size_t n, double eps, float* y, size_t ldy,
                         size_t batch, void* stream) {
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;

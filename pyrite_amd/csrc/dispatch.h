@@ -86,6 +86,32 @@ int lm_head_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t
                    float* logits, size_t ldl, int* ids, size_t batch, hipStream_t stream);
 const char* lm_last_error();
 
+// moe.hip: one Qwen3-MoE FFN layer (router, top-k, experts, combine) for
+// batch tokens; layout identical to pyrite_moe_layer of include/pyrite_hip.h.
+struct MoeLayer {
+    int router_type;
+    const void* router;
+    size_t router_len;
+    int gate_type;
+    const void* gate;
+    size_t gate_len;
+    int up_type;
+    const void* up;
+    size_t up_len;
+    int down_type;
+    const void* down;
+    size_t down_len;
+    size_t n_experts;
+    size_t hidden;
+    size_t inter;
+    size_t k;
+    int norm_topk_prob;
+    double scale;
+};
+int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, size_t ldo, int* ids_out,
+                   float* wts_out, size_t batch, hipStream_t stream);
+const char* moe_last_error();
+
 // norm.hip: RMSNorm of batch vectors of n floats (Wt may be null: weight 1).
 int rms_norm_launch(const float* X, size_t ldx, const float* Wt, size_t n, double eps, float* Y, size_t ldy,
                     size_t batch, hipStream_t stream);

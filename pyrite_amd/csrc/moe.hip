@@ -1,0 +1,626 @@
+// Qwen3-MoE FFN layer on the device, driven by device-side expert ids.
+//
+// Reference (all fp64, one token at a time): pyrite/executor.py:757-793
+// (_moe): router logits = pyrite_matvec of ffn_gate_inp (E x H), probs =
+// softmax (pyrite/tensor_ops.py:513-521), experts ranked by (-p, e), the first
+// k kept, weights renormalised when norm_topk_prob and their sum is positive,
+// scaled when expert_weights_scale != 1, then out = sum over the chosen slots
+// (in rank order, weight 0 skipped) of w * expert(x); expert(x) =
+// down . (silu(gate . x) * (up . x)) (executor.py:672-683, silu
+// tensor_ops.py:509-510).  Expert e of a stacked [E][rows][cols] GGUF tensor is
+// the contiguous byte slice e * rows * row_bytes (pyrite/qwen3_moe.py:364-398).
+//
+// Kernels, all on one stream, no host round trip:
+//   moe_router_kernel   fp64 router logits (tree order) and sum |w x| per row
+//   moe_route_kernel    per token: exact ranking (rows whose rounding
+//                       interval overlaps a top-(k+1) row are recomputed in
+//                       the reference's own order), softmax, top-k, weights;
+//                       the last token's workgroup buckets (token, slot)
+//                       pairs by expert into padded chunks of MB tokens
+//   moe_gather_kernel   activations of each bucket, zero padding
+//   moe_mv_kernel       gate and up (one launch), then down: persistent
+//                       workgroups walk (matrix, chunk, row tile) items and run
+//                       the VALU matvec body on each, weights read once per chunk
+//   moe_swiglu_kernel   act = silu(gate) * up (fp64 inside)
+//   moe_combine_kernel  out = sum of w * down-out in slot order (fp64 inside)
+#include "dequant.h"
+#include "mv_kernel.h"
+
+namespace pyrite {
+
+constexpr int kMoeMaxE = 1024;  // experts supported by the route kernel
+constexpr int kMoeMaxK = 32;    // experts per token supported
+
+// ---------------------------------------------------------------- router
+
+__global__ __launch_bounds__(256) void moe_router_kernel(int type, const uint8_t* __restrict__ W,
+                                                         unsigned long long row_bytes, int E, int H, int bs, int bpb,
+                                                         const float* __restrict__ X, unsigned long long ldx,
+                                                         double* __restrict__ logits, double* __restrict__ mags) {
+    const int b = blockIdx.y;
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (e >= E) return;
+    const uint8_t* rp = W + (unsigned long long)e * row_bytes;
+    const float* x = X + (unsigned long long)b * ldx;
+    double acc = 0.0, mag = 0.0;
+    for (int c = lane; c < H; c += 64) {
+        const int blk = c / bs;
+        const double p = dq_elem<double>(type, rp + (unsigned long long)blk * bpb, c - blk * bs) * (double)x[c];
+        acc += p;
+        mag += fabs(p);
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        acc += __shfl_xor(acc, off, 64);
+        mag += __shfl_xor(mag, off, 64);
+    }
+    if (lane == 0) {
+        logits[(unsigned long long)b * E + e] = acc;
+        mags[(unsigned long long)b * E + e] = mag;
+    }
+}
+
+// The reference's fp64 router logit of one row, computed by one wave in the
+// reference's column order (pyrite/kernels/native.c:527-553).
+__device__ double moe_ref_row(int type, const uint8_t* rp, int H, int bs, int bpb, const float* x) {
+    const int lane = threadIdx.x & 63;
+    double s = 0.0;
+    for (int base = 0; base < H; base += 64) {
+        const int c = base + lane;
+        double p = 0.0;
+        if (c < H) {
+            const int blk = c / bs;
+            p = __dmul_rn(dq_elem<double>(type, rp + (unsigned long long)blk * bpb, c - blk * bs), (double)x[c]);
+        }
+        const int n = H - base < 64 ? H - base : 64;
+        for (int k = 0; k < n; ++k) {
+            const unsigned long long u = (unsigned long long)__double_as_longlong(p);
+            const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, k);
+            const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), k);
+            s = __dadd_rn(s, __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo)));
+        }
+    }
+    return s;
+}
+
+// ---------------------------------------------------------------- routing + plan
+
+struct MoePlan {
+    int* cnt;        // [E] pairs per expert
+    int* poff;       // [E + 1] padded pair offsets (chunks of MB)
+    int* coff;       // [E + 1] chunk offsets
+    int* pair_tok;   // [max_pairs] token of each padded pair, -1 for padding
+    int* pos;        // [batch * k] padded pair index of (token, slot)
+    int* totals;     // [2]: padded pairs, chunks
+};
+
+struct MoeRouteArgs {
+    int type;
+    const uint8_t* W;
+    unsigned long long row_bytes;
+    int E, H, bs, bpb, k, MB;
+    int norm_topk;
+    double scale;
+    double gamma;  // rounding budget per unit of sum |w x|
+    const float* X;
+    unsigned long long ldx;
+    const double* logits;
+    const double* mags;
+    int* ids;          // [batch][k]
+    double* wts;       // [batch][k]
+    float* wts_out;    // [batch][k] or null
+    int* ids_out;      // [batch][k] or null (caller's copy)
+    int batch;
+    unsigned int* arrive;
+    MoePlan plan;
+};
+
+__device__ __forceinline__ bool rank_before(double la, int a, double lb, int b) {
+    return la > lb || (la == lb && a < b);
+}
+
+__global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = a.E, k = a.k;
+    __shared__ double s_l[kMoeMaxE];
+    __shared__ double s_b[kMoeMaxE];
+    __shared__ unsigned char s_mark[kMoeMaxE];
+    __shared__ unsigned char s_taken[kMoeMaxE];
+    __shared__ int s_top[kMoeMaxK + 1];
+    __shared__ double s_rv[4];
+    __shared__ int s_ri[4];
+    __shared__ int s_marked[kMoeMaxE];
+    __shared__ int s_nmarked, s_last;
+    const float* x = a.X + (unsigned long long)t * a.ldx;
+
+    for (int e = tid; e < E; e += 256) {
+        s_l[e] = a.logits[(unsigned long long)t * E + e];
+        s_b[e] = a.gamma * a.mags[(unsigned long long)t * E + e];
+        s_mark[e] = 0;
+        s_taken[e] = 0;
+    }
+    if (tid == 0) s_nmarked = 0;
+    __syncthreads();
+
+    // the first n experts in (-logit, e) order of the current values
+    auto select_top = [&](int n) {
+        for (int e = tid; e < E; e += 256) s_taken[e] = 0;
+        __syncthreads();
+        for (int s = 0; s < n; ++s) {
+            double bv = -INFINITY;
+            int bi = 0x7FFFFFFF;
+            for (int e = tid; e < E; e += 256)
+                if (!s_taken[e] && (bi == 0x7FFFFFFF || rank_before(s_l[e], e, bv, bi))) { bv = s_l[e]; bi = e; }
+            for (int off = 32; off > 0; off >>= 1) {
+                const double ov = __shfl_xor(bv, off, 64);
+                const int oi = __shfl_xor(bi, off, 64);
+                if (oi != 0x7FFFFFFF && (bi == 0x7FFFFFFF || rank_before(ov, oi, bv, bi))) { bv = ov; bi = oi; }
+            }
+            if (lane == 0) { s_rv[wave] = bv; s_ri[wave] = bi; }
+            __syncthreads();
+            if (tid == 0) {
+                double v = s_rv[0];
+                int i = s_ri[0];
+                for (int w = 1; w < 4; ++w)
+                    if (s_ri[w] != 0x7FFFFFFF && (i == 0x7FFFFFFF || rank_before(s_rv[w], s_ri[w], v, i))) {
+                        v = s_rv[w];
+                        i = s_ri[w];
+                    }
+                s_top[s] = i;
+                s_taken[i] = 1;
+            }
+            __syncthreads();
+        }
+    };
+
+    // 1. tree-order top k+1; mark every row whose interval [l - B, l + B]
+    //    meets the interval of one of them (their order is then uncertain)
+    const int kk = k + 1 <= E ? k + 1 : E;
+    select_top(kk);
+    for (int e = tid; e < E; e += 256) {
+        for (int s = 0; s < kk; ++s) {
+            const int i = s_top[s];
+            if (i == e) continue;
+            // rows whose bounds are both zero are exact (every product was zero)
+            const double bb = s_b[i] + s_b[e];
+            if ((bb > 0 && fabs(s_l[i] - s_l[e]) <= bb * (1 + 0x1p-40)) || !isfinite(s_l[e]) || !isfinite(s_l[i])) {
+                s_mark[e] = 1;
+                s_mark[i] = 1;
+            }
+        }
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 256)
+        if (s_mark[e]) s_marked[atomicAdd(&s_nmarked, 1)] = e;
+    __syncthreads();
+    // 2. recompute the marked rows exactly (one wave each), then rank again
+    for (int q = wave; q < s_nmarked; q += 4) {
+        const int e = s_marked[q];
+        const double v = moe_ref_row(a.type, a.W + (unsigned long long)e * a.row_bytes, a.H, a.bs, a.bpb, x);
+        if (lane == 0) { s_l[e] = v; s_b[e] = 0.0; }
+    }
+    __syncthreads();
+    select_top(k);
+
+    // 3. softmax of the logits (max-subtracted, summed in expert order), the
+    //    chosen probabilities, renormalisation and scale (thread 0; E and k are small)
+    if (tid == 0) {
+        double peak = s_l[0];
+        for (int e = 1; e < E; ++e) if (s_l[e] > peak) peak = s_l[e];
+        double total = 0.0;
+        for (int e = 0; e < E; ++e) total += exp(s_l[e] - peak);
+        double w[kMoeMaxK];
+        for (int s = 0; s < k; ++s) {
+            const int e = s_top[s];
+            w[s] = total <= 0.0 ? 1.0 / (double)E : exp(s_l[e] - peak) / total;
+        }
+        if (a.norm_topk) {
+            double tk = 0.0;
+            for (int s = 0; s < k; ++s) tk += w[s];
+            if (tk > 0) for (int s = 0; s < k; ++s) w[s] = w[s] / tk;
+        }
+        if (a.scale != 1.0) for (int s = 0; s < k; ++s) w[s] = w[s] * a.scale;
+        for (int s = 0; s < k; ++s) {
+            const unsigned long long o = (unsigned long long)t * k + s;
+            a.ids[o] = s_top[s];
+            a.wts[o] = w[s];
+            if (a.ids_out) a.ids_out[o] = s_top[s];
+            if (a.wts_out) a.wts_out[o] = (float)w[s];
+        }
+        __threadfence();
+        s_last = (atomicAdd(a.arrive, 1u) == (unsigned)a.batch - 1);
+        if (s_last) __threadfence();
+    }
+    __syncthreads();
+    if (!s_last) return;
+
+    // 4. plan (last workgroup): bucket the (token, slot) pairs by expert, in
+    //    token order, padded to chunks of MB
+    const MoePlan& p = a.plan;
+    for (int e = tid; e < E; e += 256) p.cnt[e] = 0;
+    __syncthreads();
+    const int npairs = a.batch * k;
+    if (tid == 0) {
+        // sequential: npairs <= 64 * 32 in practice; keeps the token order deterministic
+        for (int q = 0; q < npairs; ++q) p.cnt[a.ids[q]] += 1;
+        int po = 0, co = 0;
+        for (int e = 0; e < E; ++e) {
+            p.poff[e] = po;
+            p.coff[e] = co;
+            const int nc = (p.cnt[e] + a.MB - 1) / a.MB;
+            co += nc;
+            po += nc * a.MB;
+        }
+        p.poff[E] = po;
+        p.coff[E] = co;
+        p.totals[0] = po;
+        p.totals[1] = co;
+        for (int e = 0; e < E; ++e) p.cnt[e] = 0;
+        for (int q = 0; q < npairs; ++q) {
+            const int e = a.ids[q];
+            const int slot = p.poff[e] + p.cnt[e]++;
+            p.pair_tok[slot] = q / k;
+            p.pos[q] = slot;
+        }
+        for (int e = 0; e < E; ++e)
+            for (int q = p.poff[e] + p.cnt[e]; q < p.poff[e + 1]; ++q) p.pair_tok[q] = -1;
+        a.arrive[0] = 0u;
+    }
+}
+
+// ---------------------------------------------------------------- gather, swiglu, combine
+
+__global__ __launch_bounds__(256) void moe_gather_kernel(const float* __restrict__ X, unsigned long long ldx, int H,
+                                                         const int* __restrict__ pair_tok,
+                                                         const int* __restrict__ totals, int max_pairs,
+                                                         float* __restrict__ XG) {
+    const int npad = totals[0];
+    for (int q = blockIdx.x; q < npad && q < max_pairs; q += gridDim.x) {
+        const int t = pair_tok[q];
+        float* dst = XG + (unsigned long long)q * H;
+        for (int c = threadIdx.x; c < H; c += 256) dst[c] = t >= 0 ? X[(unsigned long long)t * ldx + c] : 0.f;
+    }
+}
+
+__global__ __launch_bounds__(256) void moe_swiglu_kernel(const float* __restrict__ G, const float* __restrict__ Uu,
+                                                         int I, const int* __restrict__ totals, int max_pairs,
+                                                         float* __restrict__ A) {
+    const unsigned long long n = (unsigned long long)(totals[0] < max_pairs ? totals[0] : max_pairs) * I;
+    for (unsigned long long i = (unsigned long long)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (unsigned long long)gridDim.x * 256) {
+        const double g = G[i];
+        const double s = g > -60.0 ? g / (1.0 + exp(-g)) : 0.0;
+        A[i] = (float)(s * (double)Uu[i]);
+    }
+}
+
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ YD, int H, int k,
+                                                          const int* __restrict__ pos, const double* __restrict__ wts,
+                                                          float* __restrict__ out, unsigned long long ldo) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= H) return;
+    double acc = 0.0;
+    for (int s = 0; s < k; ++s) {
+        const double w = wts[(unsigned long long)t * k + s];
+        if (w == 0.0) continue;
+        acc += w * (double)YD[(unsigned long long)pos[(unsigned long long)t * k + s] * H + i];
+    }
+    out[(unsigned long long)t * ldo + i] = (float)acc;
+}
+
+// ---------------------------------------------------------------- expert matvec
+
+struct MoeMat {
+    const uint8_t* W;           // stacked [E][rows][row_bytes]
+    unsigned long long slice;   // bytes per expert
+    unsigned long long row_bytes;
+    const float* X;             // [padded pairs][cols]
+    float* Y;                   // [padded pairs][rows]
+    int rows, cols, lpr_log2;
+};
+
+struct MoeMvArgs {
+    MoeMat m[2];
+    int nm;
+    int tile;                   // rows per item
+    const int* coff;            // [E + 1] chunk offsets
+    const int* poff;            // [E + 1] padded pair offsets
+    const int* totals;          // [1]: chunks
+    int E;
+};
+
+// Item i -> matrix (i / per_matrix), chunk, row tile; chunk -> expert by
+// binary search over the chunk offsets.
+template <int T, int MB, bool AL, bool XL>
+__global__ __launch_bounds__(kMvThreads) void moe_mv_kernel(const MoeMvArgs a) {
+    extern __shared__ float smem[];
+    const int chunks = a.totals[1];
+    int tiles[2];
+    long long per_m[2], total = 0;
+    for (int j = 0; j < a.nm; ++j) {
+        tiles[j] = (a.m[j].rows + a.tile - 1) / a.tile;
+        per_m[j] = (long long)chunks * tiles[j];
+        total += per_m[j];
+    }
+    for (long long it = blockIdx.x; it < total; it += gridDim.x) {
+        int j = 0;
+        long long r = it;
+        if (a.nm > 1 && r >= per_m[0]) { r -= per_m[0]; j = 1; }
+        const MoeMat& m = a.m[j];
+        const int chunk = (int)(r / tiles[j]);
+        const int tile = (int)(r - (long long)chunk * tiles[j]);
+        int lo = 0, hi = a.E;  // expert e with coff[e] <= chunk < coff[e + 1]
+        while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (a.coff[mid] <= chunk) lo = mid; else hi = mid;
+        }
+        const int e = lo;
+        const int pair0 = a.poff[e] + (chunk - a.coff[e]) * MB;
+        const int row0 = tile * a.tile;
+        MvDesc d;
+        d.W = m.W + (unsigned long long)e * m.slice + (unsigned long long)row0 * m.row_bytes;
+        d.row_bytes = m.row_bytes;
+        d.X = m.X + (unsigned long long)pair0 * m.cols;
+        d.ldx = m.cols;
+        d.Y = m.Y + (unsigned long long)pair0 * m.rows + row0;
+        d.ldy = m.rows;
+        d.rows = m.rows - row0 < a.tile ? m.rows - row0 : a.tile;
+        d.cols = m.cols;
+        d.lpr_log2 = m.lpr_log2;
+        d.wg_begin = 0;
+        d.wg_count = 1;
+        d.pad = 0;
+        d.Bnd = nullptr;
+        __syncthreads();  // the previous item's waves are done with LDS
+        mv_body<T, MB, 1, AL, XL, false>(d, 0, smem);
+    }
+}
+
+// ---------------------------------------------------------------- workspace + launch
+
+struct MoeWorkspace {
+    size_t bytes = 0;
+    char* base = nullptr;
+    unsigned int* arrive = nullptr;
+};
+
+static thread_local const char* g_moe_err = nullptr;
+const char* moe_last_error() { return g_moe_err; }
+
+static int moe_workspace(size_t bytes, hipStream_t stream, MoeWorkspace** out) {
+    static MoeWorkspace ws[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -4;
+    MoeWorkspace& w = ws[dev];
+    if (w.bytes >= bytes && w.arrive) { *out = &w; return 0; }
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+        g_moe_err = "MoE workspace must grow, which is not allowed during stream capture; run once before capturing";
+        return -4;
+    }
+    if (hipDeviceSynchronize() != hipSuccess) return -4;
+    if (w.base) (void)hipFree(w.base);
+    w.base = nullptr;
+    w.bytes = 0;
+    if (hipMalloc(&w.base, bytes) != hipSuccess) return -4;
+    w.bytes = bytes;
+    if (!w.arrive) {
+        if (hipMalloc(&w.arrive, 256) != hipSuccess) return -4;
+        if (hipMemset(w.arrive, 0, 256) != hipSuccess) return -4;
+    }
+    if (hipDeviceSynchronize() != hipSuccess) return -4;
+    *out = &w;
+    return 0;
+}
+
+// carve aligned pieces out of the workspace
+struct Carver {
+    char* p;
+    size_t used = 0;
+    template <typename U>
+    U* take(size_t n) {
+        used = (used + 255) & ~size_t(255);
+        U* r = reinterpret_cast<U*>(p ? p + used : nullptr);
+        used += n * sizeof(U);
+        return r;
+    }
+};
+
+template <int T, int MB, bool AL, bool XL>
+static hipError_t moe_mv_launch_x(const MoeMvArgs& a, size_t lds, hipStream_t s) {
+    const DevInfo& di = dev_info();
+    static const int per_cu = [] {
+        int v = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, moe_mv_kernel<T, MB, AL, XL>, kMvThreads, 0) != hipSuccess ||
+            v < 1)
+            v = 1;
+        return v;
+    }();
+    long long pc = per_cu;
+    if (lds > 0 && (long long)(di.lds_per_cu / lds) < pc) pc = (long long)(di.lds_per_cu / lds);
+    if (pc < 1) pc = 1;
+    hipLaunchKernelGGL((moe_mv_kernel<T, MB, AL, XL>), dim3((unsigned)(pc * di.cus)), dim3(kMvThreads), lds, s, a);
+    return hipGetLastError();
+}
+
+template <int T, int MB>
+static hipError_t moe_mv_launch_t(MoeMvArgs a, bool al, hipStream_t s) {
+    int max_cols = 0;
+    for (int j = 0; j < a.nm; ++j) {
+        a.m[j].lpr_log2 = plan_lpr(units_per_row<T>(a.m[j].cols));
+        max_cols = a.m[j].cols > max_cols ? a.m[j].cols : max_cols;
+    }
+    constexpr bool AQ = Geo<T>::bpb % 4 == 0;
+    if constexpr (Geo<T>::bs > 1 && MB <= 2) {
+        if (use_xl<T, MB, false>(max_cols)) {
+            const size_t lds = lds_bytes<T, MB, false>(max_cols, true);
+            return al && AQ ? moe_mv_launch_x<T, MB, AQ, true>(a, lds, s) : moe_mv_launch_x<T, MB, false, true>(a, lds, s);
+        }
+    }
+    const size_t lds = lds_bytes<T, MB, false>(max_cols, false);
+    return al && AQ ? moe_mv_launch_x<T, MB, AQ, false>(a, lds, s) : moe_mv_launch_x<T, MB, false, false>(a, lds, s);
+}
+
+static hipError_t moe_mv_launch(int type, int MB, const MoeMvArgs& a, bool al, hipStream_t s) {
+#define PYRITE_CASE(T)                                                 \
+    case T:                                                          \
+        switch (MB) {                                                \
+        case 1: return moe_mv_launch_t<T, 1>(a, al, s);              \
+        case 2: return moe_mv_launch_t<T, 2>(a, al, s);              \
+        case 4: return moe_mv_launch_t<T, 4>(a, al, s);              \
+        default: return moe_mv_launch_t<T, 8>(a, al, s);             \
+        }
+    switch (type) {
+        PYRITE_FOR_EACH_TYPE(PYRITE_CASE)
+    default: return hipErrorInvalidValue;
+    }
+#undef PYRITE_CASE
+}
+
+int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, size_t ldo, int* ids_out,
+                   float* wts_out, size_t batch, hipStream_t stream) {
+    g_moe_err = nullptr;
+    const TypeGeo gr = type_geo(L.router_type), gg = type_geo(L.gate_type), gu = type_geo(L.up_type),
+                  gd = type_geo(L.down_type);
+    if (!gr.valid || !gg.valid || !gu.valid || !gd.valid) return -1;
+    const size_t E = L.n_experts, H = L.hidden, I = L.inter, K = L.k;
+    if (E == 0 || H == 0 || I == 0 || K == 0 || K > E || E > (size_t)kMoeMaxE || K > (size_t)kMoeMaxK) return -2;
+    if (batch == 0 || batch > 4096 || H > 65536 || I > 65536) return -2;
+    if (H % gr.bs || H % gg.bs || H % gu.bs || I % gd.bs) return -2;
+    const size_t rr = H / gr.bs * gr.bpb, gs = I * (H / gg.bs * gg.bpb), us = I * (H / gu.bs * gu.bpb),
+                 ds = H * (I / gd.bs * gd.bpb);
+    if (!L.router || !L.gate || !L.up || !L.down || !X || !out) return -3;
+    if (L.router_len != E * rr || L.gate_len != E * gs || L.up_len != E * us || L.down_len != E * ds) return -3;
+    if (ldx < H || ldo < H || (reinterpret_cast<uintptr_t>(X) & 3u)) return -3;
+    // chunk width: tokens per expert chunk (weights are read once per chunk)
+    const int MB = batch == 1 ? 1 : batch <= 16 ? 2 : 4;
+    const size_t max_pairs = batch * K + E * (size_t)(MB - 1);
+
+    Carver c{nullptr};
+    auto layout = [&](Carver& cv, double** logits, double** mags, int** ids, double** wts, MoePlan* p, float** xg,
+                      float** g, float** u, float** act, float** yd) {
+        *logits = cv.take<double>(batch * E);
+        *mags = cv.take<double>(batch * E);
+        *ids = cv.take<int>(batch * K);
+        *wts = cv.take<double>(batch * K);
+        p->cnt = cv.take<int>(E);
+        p->poff = cv.take<int>(E + 1);
+        p->coff = cv.take<int>(E + 1);
+        p->pair_tok = cv.take<int>(max_pairs);
+        p->pos = cv.take<int>(batch * K);
+        p->totals = cv.take<int>(2);
+        *xg = cv.take<float>(max_pairs * H);
+        *g = cv.take<float>(max_pairs * I);
+        *u = cv.take<float>(max_pairs * I);
+        *act = cv.take<float>(max_pairs * I);
+        *yd = cv.take<float>(max_pairs * H);
+    };
+    double *logits, *mags, *wts;
+    int* ids;
+    MoePlan plan;
+    float *xg, *g, *u, *act, *yd;
+    layout(c, &logits, &mags, &ids, &wts, &plan, &xg, &g, &u, &act, &yd);
+    MoeWorkspace* ws = nullptr;
+    if (const int rc = moe_workspace(c.used + 256, stream, &ws)) return rc;
+    Carver cw{ws->base};
+    layout(cw, &logits, &mags, &ids, &wts, &plan, &xg, &g, &u, &act, &yd);
+
+    // 1. router
+    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)((E + 3) / 4), (unsigned)batch), dim3(256), 0, stream,
+                       L.router_type, static_cast<const uint8_t*>(L.router), (unsigned long long)rr, (int)E, (int)H,
+                       gr.bs, gr.bpb, X, (unsigned long long)ldx, logits, mags);
+    if (hipGetLastError() != hipSuccess) return -4;
+    // 2. route + plan
+    MoeRouteArgs ra;
+    ra.type = L.router_type;
+    ra.W = static_cast<const uint8_t*>(L.router);
+    ra.row_bytes = rr;
+    ra.E = (int)E;
+    ra.H = (int)H;
+    ra.bs = gr.bs;
+    ra.bpb = gr.bpb;
+    ra.k = (int)K;
+    ra.MB = MB;
+    ra.norm_topk = L.norm_topk_prob;
+    ra.scale = L.scale;
+    {
+        // tree sums of <= H/64 + 6 adds per lane path, the reference's sequential sum of H terms
+        const double u64 = 1.0 / 9007199254740992.0;
+        const double d1 = (double)H / 64 + 8, d2 = (double)H;
+        ra.gamma = (d1 * u64 / (1 - d1 * u64) + d2 * u64 / (1 - d2 * u64)) * (1 + 1.0 / 1024);
+    }
+    ra.X = X;
+    ra.ldx = ldx;
+    ra.logits = logits;
+    ra.mags = mags;
+    ra.ids = ids;
+    ra.wts = wts;
+    ra.wts_out = wts_out;
+    ra.ids_out = ids_out;
+    ra.batch = (int)batch;
+    ra.arrive = ws->arrive;
+    ra.plan = plan;
+    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)batch), dim3(256), 0, stream, ra);
+    if (hipGetLastError() != hipSuccess) return -4;
+    // 3. gather
+    const unsigned gblocks = (unsigned)(max_pairs < 4096 ? max_pairs : 4096);
+    hipLaunchKernelGGL(moe_gather_kernel, dim3(gblocks), dim3(256), 0, stream, X, (unsigned long long)ldx, (int)H,
+                       plan.pair_tok, plan.totals, (int)max_pairs, xg);
+    if (hipGetLastError() != hipSuccess) return -4;
+    // 4. gate and up
+    auto tile_for = [&](size_t rows) {
+        // aim for ~2048 items per launch at the worst-case chunk count
+        const size_t chunks = (batch * K + MB - 1) / MB;
+        size_t t = 16;
+        while (t < 128 && chunks * ((rows + t - 1) / t) > 2048) t *= 2;
+        return (int)t;
+    };
+    const bool al_gu = ((reinterpret_cast<uintptr_t>(L.gate) | reinterpret_cast<uintptr_t>(L.up)) & 3u) == 0;
+    MoeMvArgs ma;
+    ma.coff = plan.coff;
+    ma.poff = plan.poff;
+    ma.totals = plan.totals;
+    ma.E = (int)E;
+    auto mat = [&](const void* W, size_t slice, const TypeGeo& tg, const float* Xs, float* Ys, size_t rows, size_t cols) {
+        MoeMat m;
+        m.W = static_cast<const uint8_t*>(W);
+        m.slice = slice;
+        m.row_bytes = cols / tg.bs * tg.bpb;
+        m.X = Xs;
+        m.Y = Ys;
+        m.rows = (int)rows;
+        m.cols = (int)cols;
+        m.lpr_log2 = 0;
+        return m;
+    };
+    ma.tile = tile_for(I);
+    if (L.gate_type == L.up_type) {
+        ma.nm = 2;
+        ma.m[0] = mat(L.gate, gs, gg, xg, g, I, H);
+        ma.m[1] = mat(L.up, us, gu, xg, u, I, H);
+        if (moe_mv_launch(L.gate_type, MB, ma, al_gu, stream) != hipSuccess) return -4;
+    } else {
+        ma.nm = 1;
+        ma.m[0] = mat(L.gate, gs, gg, xg, g, I, H);
+        if (moe_mv_launch(L.gate_type, MB, ma, al_gu, stream) != hipSuccess) return -4;
+        ma.m[0] = mat(L.up, us, gu, xg, u, I, H);
+        if (moe_mv_launch(L.up_type, MB, ma, al_gu, stream) != hipSuccess) return -4;
+    }
+    // 5. SwiGLU
+    hipLaunchKernelGGL(moe_swiglu_kernel, dim3(1024), dim3(256), 0, stream, g, u, (int)I, plan.totals,
+                       (int)max_pairs, act);
+    if (hipGetLastError() != hipSuccess) return -4;
+    // 6. down
+    ma.nm = 1;
+    ma.tile = tile_for(H);
+    ma.m[0] = mat(L.down, ds, gd, act, yd, H, I);
+    if (moe_mv_launch(L.down_type, MB, ma, (reinterpret_cast<uintptr_t>(L.down) & 3u) == 0, stream) != hipSuccess)
+        return -4;
+    // 7. combine
+    hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)batch), dim3(256), 0, stream,
+                       yd, (int)H, (int)K, plan.pos, wts, out, (unsigned long long)ldo);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+}  // namespace pyrite

@@ -7,6 +7,9 @@ include/pyrite_hip.h.
 """
 from __future__ import annotations
 
+import ctypes
+from dataclasses import dataclass
+
 import torch
 
 from . import _lib
@@ -106,3 +109,72 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor | None = None, eps: float = 1
                                    n, float(eps), y.data_ptr(), _ld(y), x2.shape[0], _stream_ptr(x2.device))
     _lib.check(code, "pyrite_dev_rms_norm")
     return y.reshape(x.shape)
+
+
+class _MoeLayerC(ctypes.Structure):
+    _fields_ = [
+        ("router_type", ctypes.c_int), ("router", ctypes.c_void_p), ("router_len", ctypes.c_size_t),
+        ("gate_type", ctypes.c_int), ("gate", ctypes.c_void_p), ("gate_len", ctypes.c_size_t),
+        ("up_type", ctypes.c_int), ("up", ctypes.c_void_p), ("up_len", ctypes.c_size_t),
+        ("down_type", ctypes.c_int), ("down", ctypes.c_void_p), ("down_len", ctypes.c_size_t),
+        ("n_experts", ctypes.c_size_t), ("hidden", ctypes.c_size_t), ("inter", ctypes.c_size_t),
+        ("k", ctypes.c_size_t), ("norm_topk_prob", ctypes.c_int), ("scale", ctypes.c_double),
+    ]
+
+
+@dataclass
+class MoeLayer:
+    """One Qwen3-MoE FFN layer's tensors in device memory (verbatim GGUF bytes).
+
+    ``router`` is ffn_gate_inp [n_experts][hidden]; ``gate``/``up`` are the
+    stacked [n_experts][inter][hidden] tensors and ``down`` [n_experts][hidden][inter]
+    (pyrite/qwen3_moe.py:364-398, 432-443).
+    """
+    router_type: int
+    router: torch.Tensor
+    gate_type: int
+    gate: torch.Tensor
+    up_type: int
+    up: torch.Tensor
+    down_type: int
+    down: torch.Tensor
+    n_experts: int
+    hidden: int
+    inter: int
+    k: int
+    norm_topk_prob: bool = True
+    scale: float = 1.0
+
+    def _c(self) -> _MoeLayerC:
+        for t in (self.router, self.gate, self.up, self.down):
+            if t.dtype != torch.uint8 or not t.is_cuda or not t.is_contiguous():
+                raise ValueError("MoE tensors must be contiguous uint8 CUDA tensors")
+        return _MoeLayerC(self.router_type, self.router.data_ptr(), self.router.numel(),
+                          self.gate_type, self.gate.data_ptr(), self.gate.numel(),
+                          self.up_type, self.up.data_ptr(), self.up.numel(),
+                          self.down_type, self.down.data_ptr(), self.down.numel(),
+                          self.n_experts, self.hidden, self.inter, self.k, int(self.norm_topk_prob),
+                          float(self.scale))
+
+
+def moe_ffn(layer: MoeLayer, x: torch.Tensor, out: torch.Tensor | None = None
+            ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Qwen3-MoE FFN for fp32 tokens x [batch, hidden] (pyrite/executor.py:757-793).
+
+    Returns (out [batch, hidden] fp32, ids [batch, k] int32 in rank order,
+    weights [batch, k] fp32); the ids equal the reference's expert choice.
+    """
+    x2 = x.reshape(1, -1) if x.dim() == 1 else x
+    if x2.dtype != torch.float32 or x2.shape[1] != layer.hidden or x2.stride(1) != 1 or not x2.is_cuda:
+        raise ValueError("x must be an fp32 CUDA tensor [batch, hidden] with contiguous rows")
+    batch = x2.shape[0]
+    if out is None:
+        out = torch.empty(batch, layer.hidden, dtype=torch.float32, device=x2.device)
+    ids = torch.empty(batch, layer.k, dtype=torch.int32, device=x2.device)
+    wts = torch.empty(batch, layer.k, dtype=torch.float32, device=x2.device)
+    c = layer._c()
+    lib = _lib.load()
+    code = lib.pyrite_dev_moe_ffn(ctypes.addressof(c), x2.data_ptr(), _ld(x2), out.data_ptr(), _ld(out),
+                                  ids.data_ptr(), wts.data_ptr(), batch, _stream_ptr(x2.device))
+    _lib.check(code, "pyrite_dev_moe_ffn")
+    return out, ids, wts

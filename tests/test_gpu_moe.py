@@ -1,0 +1,132 @@
+"""GPU parity of the Qwen3-MoE FFN layer (pyrite/executor.py:757-793, 672-683).
+
+The oracle (oracle_moe_ffn) restates the reference's fp64 layer: router matvec,
+softmax, (-p, e) ranking, top-k, renormalisation, scale, SwiGLU experts and the
+weighted sum in rank order.  The expert ids must be identical; the routing
+weights match to fp32 rounding; the output is within 1e-4 of its largest
+magnitude (fp32 matvecs against the fp64 reference).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from tests.gpu_util import announce
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from pyrite_amd import _lib
+    _lib.load()
+    return torch.device("cuda:0")
+
+
+def _payload(rng, t, n_rows, cols):
+    from tests.golden.make_golden import random_payload
+    return random_payload(rng, t, n_rows, cols)
+
+
+def _fast_random(rng, t, rows, cols):
+    """Random block bytes with finite, moderate fp16 scales (vectorised)."""
+    from oracle.oracle import TYPES
+    _, bs, bpb = TYPES[t]
+    raw = rng.integers(0, 256, size=rows * (cols // bs) * bpb, dtype=np.uint8).reshape(-1, bpb)
+    halves = {12: (0, 2), 13: (0, 2), 14: (208,), 10: (80, 82), 11: (108,), 23: (0,), 2: (0,), 8: (0,)}[t]
+    for off in halves:
+        raw[:, off + 1] &= 0x3B  # exponent field below 0x1E: finite and at most ~1
+    return raw.reshape(-1)
+
+
+def _layer(orc, rng, E, H, I, k, types=(0, 12, 12, 14), seed=1, norm=True, scale=1.0):
+    from pyrite_amd import device
+    rt, gt, ut, dt = types
+    router = orc.normal(seed, E * H, 0.0, 0.02).astype(np.float32).view(np.uint8).copy() if rt == 0 else \
+        _fast_random(rng, rt, E, H)
+    gate = _fast_random(rng, gt, E * I, H)
+    up = _fast_random(rng, ut, E * I, H)
+    down = _fast_random(rng, dt, E * H, I)
+    d = torch.device("cuda:0")
+    layer = device.MoeLayer(rt, torch.from_numpy(router).to(d), gt, torch.from_numpy(gate).to(d),
+                            ut, torch.from_numpy(up).to(d), dt, torch.from_numpy(down).to(d),
+                            E, H, I, k, norm, scale)
+    return layer, (router, gate, up, down)
+
+
+def _check(orc, layer, host, xs, what):
+    from pyrite_amd import device
+    router, gate, up, down = host
+    announce("moe", what, f"E={layer.n_experts}", f"H={layer.hidden}", f"I={layer.inter}", f"k={layer.k}",
+             f"batch={xs.shape[0]}")
+    out, ids, wts = device.moe_ffn(layer, torch.from_numpy(np.ascontiguousarray(xs)).to("cuda:0"))
+    torch.cuda.synchronize()
+    out, ids, wts = out.cpu().numpy(), ids.cpu().numpy(), wts.cpu().numpy()
+    for b in range(xs.shape[0]):
+        ref, rids, rw, _ = orc.moe_ffn(router, layer.router_type, gate, layer.gate_type, up, layer.up_type,
+                                       down, layer.down_type, layer.n_experts, layer.hidden, layer.inter,
+                                       layer.k, xs[b].astype(np.float64), layer.norm_topk_prob, layer.scale)
+        assert list(ids[b]) == list(rids), f"{what} b={b}: ids {list(ids[b])} != {list(rids)}"
+        np.testing.assert_allclose(wts[b], rw, rtol=2e-7, atol=1e-30, err_msg=f"{what} b={b} weights")
+        scale = float(np.max(np.abs(ref))) if ref.size else 0.0
+        err = float(np.max(np.abs(out[b].astype(np.float64) - ref)))
+        assert err <= 1e-4 * scale + 1e-30, f"{what} b={b}: max err {err} vs scale {scale}"
+    return ids
+
+
+@pytest.mark.parametrize("batch", [1, 5, 20])
+def test_moe_small(orc, dev, batch):
+    rng = np.random.default_rng(100 + batch)
+    layer, host = _layer(orc, rng, 16, 256, 256, 4, seed=7 + batch)
+    xs = np.stack([orc.normal(500 + b, 256) for b in range(batch)])
+    _check(orc, layer, host, xs, "small")
+
+
+@pytest.mark.parametrize("norm,scale", [(False, 1.0), (True, 2.5), (False, 0.5)])
+def test_moe_weight_options(orc, dev, norm, scale):
+    rng = np.random.default_rng(200)
+    layer, host = _layer(orc, rng, 32, 512, 256, 6, seed=21, norm=norm, scale=scale)
+    xs = np.stack([orc.normal(600 + b, 512) for b in range(3)])
+    _check(orc, layer, host, xs, f"norm={norm} scale={scale}")
+
+
+def test_moe_other_types(orc, dev):
+    rng = np.random.default_rng(300)
+    layer, host = _layer(orc, rng, 16, 512, 256, 4, types=(0, 13, 23, 11), seed=31)
+    xs = np.stack([orc.normal(700 + b, 512) for b in range(4)])
+    _check(orc, layer, host, xs, "Q5_K/IQ4_XS/Q3_K")
+
+
+def test_moe_router_ties(orc, dev):
+    """Duplicate router rows: equal logits, the lower expert index ranks first."""
+    rng = np.random.default_rng(400)
+    E, H = 32, 512
+    layer, host = _layer(orc, rng, E, H, 256, 8, seed=41)
+    router = host[0].view(np.float32).reshape(E, H).copy()
+    x = orc.normal(800, H)
+    logits = router.astype(np.float64) @ x.astype(np.float64)
+    top = int(np.argmax(logits))
+    for dst in (0, 5, 17, 31):
+        if dst != top:
+            router[dst] = router[top]
+    # near tie: one weight changed by one ulp
+    near = (top + 9) % E
+    router[near] = router[top]
+    router[near, 3] = np.nextafter(router[near, 3], np.float32(np.inf))
+    rbytes = router.view(np.uint8).reshape(-1).copy()
+    layer.router = torch.from_numpy(rbytes).to("cuda:0")
+    ids = _check(orc, layer, (rbytes,) + host[1:], x[None, :], "ties")
+    assert len(set(ids[0].tolist())) == 8
+
+
+def test_moe_qwen3_30b_shape(orc, dev):
+    """Qwen3-30B-A3B MoE shape: 128 experts, hidden 2048, moe_intermediate 768, top-8."""
+    rng = np.random.default_rng(20244)
+    layer, host = _layer(orc, rng, 128, 2048, 768, 8, seed=20244000)
+    for batch in (1, 8, 64):
+        xs = np.stack([orc.normal(20244100 + b, 2048) for b in range(batch)])
+        _check(orc, layer, host, xs, f"qwen3-30b b={batch}")
