@@ -19,6 +19,12 @@ stream right after the timed replay.
 
 Prints one JSON line.  value = quantized weight bytes / second over the timed
 steps (GB/s).  --gpus N > 1 exits: this path runs on one GPU.
+
+The line also carries, under "configs", the other configurations of the
+path, each timed as calls captured in one HIP graph: the single Q4_K
+3072x1024 matvec, the Q6_K 151936x1024 LM head with its exact greedy id, the
+Qwen3-30B-A3B MoE layer (tokens/s at batch 1, 8, 64) and the Llama-3-8B
+Q4_K_M layer (batch-1 decode and 512-token prefill).
 """
 from __future__ import annotations
 
@@ -116,6 +122,163 @@ def run_cpu_baseline(weights, np, budget_s: float):
                       f"single-vector calls) through pyrite_matvec, single thread, {dt:.1f} s"}
 
 
+# ---------------------------------------------------------------- other configurations
+# Each is timed as `reps` calls captured in one HIP graph (replayed once after
+# a warm-up replay), over rotated weight copies or varying inputs so that
+# weights come from HBM rather than the 256 MB Infinity Cache.
+
+def time_graph(torch, stream, calls, check=None) -> float:
+    """Seconds per call for a list of zero-argument callables captured in one graph."""
+    for c in (calls if check else calls[:2]):
+        c()  # eager warm-up (workspaces are sized outside capture) and the reference for the check
+    torch.cuda.synchronize()
+    eager = check() if check else None
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for c in calls:
+            c()
+    g.replay()
+    torch.cuda.synchronize()
+    if check is not None:
+        again = check()
+        for a, b in zip(eager, again):
+            if not torch.equal(a, b):
+                raise RuntimeError("graph replay differs from the eager calls")
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / len(calls)
+
+
+def quantized_normal(np, quantize, t, n, seed):
+    rng = np.random.default_rng(seed)
+    w = (rng.standard_normal(n, dtype=np.float32) * np.float32(0.02)).astype(np.float64)
+    return quantize(t, w)
+
+
+def bench_config1(torch, np, quantize, stream, device):
+    """Single Q4_K 3072x1024 matvec (Qwen3-0.6B ffn_up), batch 1."""
+    rows, cols = 3072, 1024
+    p = quantized_normal(np, quantize, 12, rows * cols, SEED + 11)
+    ws = [torch.from_numpy(p).cuda() for _ in range(160)]  # 283 MB of copies
+    x = torch.randn(1, cols, device="cuda")
+    y = torch.empty(1, rows, device="cuda")
+    calls = [lambda w=w: device.matvec(12, w, x, rows, cols, out=y) for w in ws]
+    dt = time_graph(torch, stream, calls)
+    return {"workload": "Q4_K 3072x1024 matvec, batch 1", "us": round(dt * 1e6, 3),
+            "gbs": round(p.nbytes / dt / 1e9, 1), "pct_hbm_peak": round(100 * p.nbytes / dt / 1e9 / HBM_PEAK_GBS, 2)}
+
+
+def bench_lm_head(torch, np, quantize, stream, device):
+    """Qwen3 LM head: Q6_K 151936x1024, RMS-normalised N(0,1) input, logits + greedy id."""
+    rows, cols = 151936, 1024
+    p = quantized_normal(np, quantize, 14, rows * cols, SEED + 12)
+    ws = [torch.from_numpy(p).cuda() for _ in range(3)]
+    rng = np.random.default_rng(SEED + 13)
+    xs = []
+    for _ in range(6):
+        h = rng.standard_normal(cols)
+        xs.append(torch.from_numpy((h / np.sqrt(np.mean(h * h) + 1e-6)).astype(np.float32)[None, :]).cuda())
+    logits = torch.empty(1, rows, device="cuda")
+    ids = []
+
+    def head(i):
+        _, idt = device.lm_head_argmax(14, ws[i % 3], xs[i % 6], rows, cols, logits=logits)
+        ids.append(idt)
+    reps = 24
+    dt_head = time_graph(torch, stream, [lambda i=i: head(i) for i in range(reps)])
+    dt_mv = time_graph(torch, stream, [lambda i=i: device.matvec(14, ws[i % 3], xs[i % 6], rows, cols, out=logits)
+                                       for i in range(reps)])
+    return {"workload": "Q6_K 151936x1024 LM head, batch 1 (logits + exact greedy id)",
+            "us_per_token": round(dt_head * 1e6, 2), "tokens_per_s": round(1 / dt_head, 1),
+            "gbs": round(p.nbytes / dt_head / 1e9, 1),
+            "pct_hbm_peak": round(100 * p.nbytes / dt_head / 1e9 / HBM_PEAK_GBS, 2),
+            "matvec_only_us": round(dt_mv * 1e6, 2), "matvec_only_gbs": round(p.nbytes / dt_mv / 1e9, 1),
+            "bytes_per_token": p.nbytes}
+
+
+def bench_moe(torch, np, quantize, stream, device, distinct_experts: int = 8):
+    """Qwen3-30B-A3B MoE FFN: 128 experts, hidden 2048, inter 768, top-8; batch 1, 8, 64."""
+    E, H, I, K = 128, 2048, 768, 8
+    rng = np.random.default_rng(SEED + 14)
+    router = (rng.standard_normal(E * H, dtype=np.float32) * np.float32(0.02)).view(np.uint8).copy()
+    # distinct_experts seeded quantized experts, tiled over the 128 expert slices
+    g = [quantized_normal(np, quantize, 12, I * H, SEED + 100 + e) for e in range(distinct_experts)]
+    u = [quantized_normal(np, quantize, 12, I * H, SEED + 200 + e) for e in range(distinct_experts)]
+    d = [quantized_normal(np, quantize, 14, H * I, SEED + 300 + e) for e in range(distinct_experts)]
+    gate = np.concatenate([g[e % distinct_experts] for e in range(E)])
+    up = np.concatenate([u[e % distinct_experts] for e in range(E)])
+    down = np.concatenate([d[e % distinct_experts] for e in range(E)])
+    slice_bytes = g[0].nbytes + u[0].nbytes + d[0].nbytes
+    layers = []
+    for _ in range(2):  # two copies of the whole layer (862 MB), alternated
+        layers.append(device.MoeLayer(0, torch.from_numpy(router).cuda(), 12, torch.from_numpy(gate).cuda(),
+                                      12, torch.from_numpy(up).cuda(), 14, torch.from_numpy(down).cuda(),
+                                      E, H, I, K, True, 1.0))
+    out = {}
+    for batch in (1, 8, 64):
+        reps = 16
+        xs = [torch.from_numpy(rng.standard_normal((batch, H), dtype=np.float32)).cuda() for _ in range(reps)]
+        ys = [torch.empty(batch, H, device="cuda") for _ in range(reps)]
+        holder = {}
+
+        def call(i):
+            _, ids, _ = device.moe_ffn(layers[i % 2], xs[i], out=ys[i])
+            holder[i] = ids
+        dt = time_graph(torch, stream, [lambda i=i: call(i) for i in range(reps)], check=lambda: [y.clone() for y in ys])
+        distinct = [len(set(holder[i].cpu().numpy().reshape(-1).tolist())) for i in range(reps)]
+        nbytes = float(np.mean(distinct)) * slice_bytes + router.nbytes
+        out[f"b{batch}"] = {"us_per_layer": round(dt * 1e6, 2), "tokens_per_s": round(batch / dt, 1),
+                            "distinct_experts": round(float(np.mean(distinct)), 2),
+                            "gbs": round(nbytes / dt / 1e9, 1),
+                            "pct_hbm_peak": round(100 * nbytes / dt / 1e9 / HBM_PEAK_GBS, 2)}
+    out["workload"] = ("Qwen3-30B-A3B MoE FFN layer: router F32 2048x128, gate/up Q4_K [128x768x2048], "
+                       f"down Q6_K [128x2048x768], top-8, renormalised; {distinct_experts} seeded quantized "
+                       "experts tiled over the 128 slices, 2 layer copies alternated, distinct inputs per call")
+    return out
+
+
+def bench_llama(torch, np, quantize, stream, device, lib, sptr):
+    """Llama-3-8B layer in Q4_K_M mix: decode (batch 1) and 512-token prefill."""
+    shapes = [("q", 12, 4096, 4096), ("k", 12, 1024, 4096), ("v", 12, 1024, 4096), ("o", 12, 4096, 4096),
+              ("gate", 12, 14336, 4096), ("up", 12, 14336, 4096), ("down", 14, 4096, 14336)]
+    cache = {}
+    mats = []
+    for name, t, rows, cols in shapes:
+        key = (t, rows, cols)
+        if key not in cache:
+            cache[key] = quantized_normal(np, quantize, t, rows * cols, SEED + 20 + len(cache))
+        mats.append((name, t, rows, cols, cache[key]))
+    layer_bytes = sum(m[4].nbytes for m in mats)
+    copies = 3
+    dev = [[torch.from_numpy(m[4]).cuda() for m in mats] for _ in range(copies)]
+    res = {"workload": "Llama-3-8B layer, Q4_K_M mix: q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096 Q4_K, "
+                       "down 4096x14336 Q6_K", "bytes_per_layer": layer_bytes}
+    for batch, reps in ((1, 12), (512, 2)):
+        xs = {c: torch.randn(batch, c, device="cuda") for c in (4096, 14336)}
+        ys = [torch.empty(batch, m[2], device="cuda") for m in mats]
+
+        def layer(i):
+            ws = dev[i % copies]
+            q4 = [j for j, m in enumerate(mats) if m[1] == 12]
+            arr = (Desc * len(q4))()
+            for a, j in enumerate(q4):
+                _, t, rows, cols, p = mats[j]
+                arr[a] = Desc(ws[j].data_ptr(), p.nbytes, rows, cols, xs[cols].data_ptr(), cols, ys[j].data_ptr(), rows)
+            rc = lib.pyrite_dev_matvec_grouped(12, arr, len(q4), batch, sptr)
+            if rc != 0:
+                raise RuntimeError(f"grouped matvec failed: {rc} {lib.pyrite_hip_last_error()}")
+            j = len(mats) - 1
+            device.matvec(14, ws[j], xs[14336], mats[j][2], mats[j][3], out=ys[j])
+        dt = time_graph(torch, stream, [lambda i=i: layer(i) for i in range(reps)])
+        flops = 2.0 * batch * sum(m[2] * m[3] for m in mats)
+        key = "decode_b1" if batch == 1 else "prefill_512"
+        res[key] = {"us": round(dt * 1e6, 2), "gbs": round(layer_bytes / dt / 1e9, 1),
+                    "pct_hbm_peak": round(100 * layer_bytes / dt / 1e9 / HBM_PEAK_GBS, 2),
+                    "tflops": round(flops / dt / 1e12, 2)}
+    return res
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -123,6 +286,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extra", action="store_true", help="skip the LM-head, MoE and Llama configurations")
+    ap.add_argument("--only", default=None,
+                    help="run only the named extra configuration (config1_q4k_3072x1024, config3_lm_head, "
+                         "config4_moe, config5_llama3_8b_layer) and print its JSON; for profiling")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures the dequant-matvec path on one GPU; runs on more than one GPU "
@@ -138,6 +305,17 @@ def main() -> int:
     lib = _lib.load()
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
+    if args.only:
+        from pyrite_amd import device
+        stream = torch.cuda.Stream()
+        torch.cuda.set_stream(stream)
+        sptr = ctypes.c_void_p(stream.cuda_stream)
+        fns = {"config1_q4k_3072x1024": lambda: bench_config1(torch, np, quantize, stream, device),
+               "config3_lm_head": lambda: bench_lm_head(torch, np, quantize, stream, device),
+               "config4_moe": lambda: bench_moe(torch, np, quantize, stream, device),
+               "config5_llama3_8b_layer": lambda: bench_llama(torch, np, quantize, stream, device, lib, sptr)}
+        print(json.dumps({args.only: fns[args.only]()}), flush=True)
+        return 0
     log("quantizing and uploading the sweep weights")
     weights, bytes_per_set = build_weights(torch, np, quantize)
     rng = np.random.default_rng(SEED + 1)
@@ -242,6 +420,19 @@ def main() -> int:
                 "avg_launch_us": round(dk["avg_us"], 3), "bytes_per_launch": dk["bytes_per_launch"],
                 "timing": timing_source}
 
+    extra = None
+    if not args.no_extra:
+        from pyrite_amd import device
+        extra = {}
+        for name, fn in (("config1_q4k_3072x1024", lambda: bench_config1(torch, np, quantize, stream, device)),
+                         ("config3_lm_head", lambda: bench_lm_head(torch, np, quantize, stream, device)),
+                         ("config4_moe", lambda: bench_moe(torch, np, quantize, stream, device)),
+                         ("config5_llama3_8b_layer", lambda: bench_llama(torch, np, quantize, stream, device, lib,
+                                                                         sptr))):
+            log(f"extra configuration: {name}")
+            extra[name] = fn()
+            torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu_baseline:
         log(f"cpu baseline (~{args.cpu_seconds:.0f} s)")
@@ -272,6 +463,7 @@ def main() -> int:
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "configs": extra,
         "per_kernel": {k: {kk: round(vv, 3) if isinstance(vv, float) else vv for kk, vv in v.items()}
                        for k, v in sorted(per_kernel.items())},
     }
