@@ -33,22 +33,34 @@ constexpr int kMoeMaxK = 32;    // experts per token supported
 
 // ---------------------------------------------------------------- router
 
-__global__ __launch_bounds__(256) void moe_router_kernel(int type, const uint8_t* __restrict__ W,
-                                                         unsigned long long row_bytes, int E, int H, int bs, int bpb,
-                                                         const float* __restrict__ X, unsigned long long ldx,
-                                                         double* __restrict__ logits, double* __restrict__ mags) {
+// One wave per (expert row, token).  F32 routers (the Qwen3 case) read 4
+// weights per lane per load; other types decode element by element.
+__global__ __launch_bounds__(64) void moe_router_kernel(int type, const uint8_t* __restrict__ W,
+                                                        unsigned long long row_bytes, int E, int H, int bs, int bpb,
+                                                        const float* __restrict__ X, unsigned long long ldx,
+                                                        double* __restrict__ logits, double* __restrict__ mags) {
     const int b = blockIdx.y;
-    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (e >= E) return;
+    const int e = blockIdx.x;
+    const int lane = threadIdx.x;
     const uint8_t* rp = W + (unsigned long long)e * row_bytes;
     const float* x = X + (unsigned long long)b * ldx;
     double acc = 0.0, mag = 0.0;
-    for (int c = lane; c < H; c += 64) {
-        const int blk = c / bs;
-        const double p = dq_elem<double>(type, rp + (unsigned long long)blk * bpb, c - blk * bs) * (double)x[c];
-        acc += p;
-        mag += fabs(p);
+    if (type == T_F32 && (H & 3) == 0 && ((reinterpret_cast<uintptr_t>(rp) | reinterpret_cast<uintptr_t>(x)) & 15) == 0) {
+        const float4* w4 = reinterpret_cast<const float4*>(rp);
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        for (int c = lane; c < H / 4; c += 64) {
+            const float4 w = w4[c], v = x4[c];
+            const double p0 = (double)w.x * v.x, p1 = (double)w.y * v.y, p2 = (double)w.z * v.z, p3 = (double)w.w * v.w;
+            acc += (p0 + p1) + (p2 + p3);
+            mag += (fabs(p0) + fabs(p1)) + (fabs(p2) + fabs(p3));
+        }
+    } else {
+        for (int c = lane; c < H; c += 64) {
+            const int blk = c / bs;
+            const double p = dq_elem<double>(type, rp + (unsigned long long)blk * bpb, c - blk * bs) * (double)x[c];
+            acc += p;
+            mag += fabs(p);
+        }
     }
     for (int off = 32; off > 0; off >>= 1) {
         acc += __shfl_xor(acc, off, 64);
@@ -125,63 +137,44 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     __shared__ double s_l[kMoeMaxE];
     __shared__ double s_b[kMoeMaxE];
     __shared__ unsigned char s_mark[kMoeMaxE];
-    __shared__ unsigned char s_taken[kMoeMaxE];
     __shared__ int s_top[kMoeMaxK + 1];
-    __shared__ double s_rv[4];
-    __shared__ int s_ri[4];
     __shared__ int s_marked[kMoeMaxE];
+    __shared__ double s_red[4];
+    __shared__ int s_poff[kMoeMaxE + 1];
     __shared__ int s_nmarked, s_last;
     const float* x = a.X + (unsigned long long)t * a.ldx;
 
+    // NaN logits rank last (as -inf), keeping the ranks a total order
     for (int e = tid; e < E; e += 256) {
-        s_l[e] = a.logits[(unsigned long long)t * E + e];
+        const double l = a.logits[(unsigned long long)t * E + e];
+        s_l[e] = isnan(l) ? -INFINITY : l;
         s_b[e] = a.gamma * a.mags[(unsigned long long)t * E + e];
         s_mark[e] = 0;
-        s_taken[e] = 0;
     }
     if (tid == 0) s_nmarked = 0;
     __syncthreads();
 
-    // the first n experts in (-logit, e) order of the current values
-    auto select_top = [&](int n) {
-        for (int e = tid; e < E; e += 256) s_taken[e] = 0;
-        __syncthreads();
-        for (int s = 0; s < n; ++s) {
-            double bv = -INFINITY;
-            int bi = 0x7FFFFFFF;
-            for (int e = tid; e < E; e += 256)
-                if (!s_taken[e] && (bi == 0x7FFFFFFF || rank_before(s_l[e], e, bv, bi))) { bv = s_l[e]; bi = e; }
-            for (int off = 32; off > 0; off >>= 1) {
-                const double ov = __shfl_xor(bv, off, 64);
-                const int oi = __shfl_xor(bi, off, 64);
-                if (oi != 0x7FFFFFFF && (bi == 0x7FFFFFFF || rank_before(ov, oi, bv, bi))) { bv = ov; bi = oi; }
-            }
-            if (lane == 0) { s_rv[wave] = bv; s_ri[wave] = bi; }
-            __syncthreads();
-            if (tid == 0) {
-                double v = s_rv[0];
-                int i = s_ri[0];
-                for (int w = 1; w < 4; ++w)
-                    if (s_ri[w] != 0x7FFFFFFF && (i == 0x7FFFFFFF || rank_before(s_rv[w], s_ri[w], v, i))) {
-                        v = s_rv[w];
-                        i = s_ri[w];
-                    }
-                s_top[s] = i;
-                s_taken[i] = 1;
-            }
-            __syncthreads();
+    // rank of every expert in (-logit, e) order (a total order: ranks are
+    // unique); the first n land in s_top
+    auto rank_top = [&](int n) {
+        for (int e = tid; e < E; e += 256) {
+            const double le = s_l[e];
+            int r = 0;
+            for (int j = 0; j < E; ++j) r += rank_before(s_l[j], j, le, e);
+            if (r < n) s_top[r] = e;
         }
+        __syncthreads();
     };
 
     // 1. tree-order top k+1; mark every row whose interval [l - B, l + B]
-    //    meets the interval of one of them (their order is then uncertain)
+    //    meets the interval of one of them (their order is then uncertain;
+    //    rows whose bounds are both zero are exact)
     const int kk = k + 1 <= E ? k + 1 : E;
-    select_top(kk);
+    rank_top(kk);
     for (int e = tid; e < E; e += 256) {
-        for (int s = 0; s < kk; ++s) {
-            const int i = s_top[s];
+        for (int q = 0; q < kk; ++q) {
+            const int i = s_top[q];
             if (i == e) continue;
-            // rows whose bounds are both zero are exact (every product was zero)
             const double bb = s_b[i] + s_b[e];
             if ((bb > 0 && fabs(s_l[i] - s_l[e]) <= bb * (1 + 0x1p-40)) || !isfinite(s_l[e]) || !isfinite(s_l[i])) {
                 s_mark[e] = 1;
@@ -194,38 +187,49 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
         if (s_mark[e]) s_marked[atomicAdd(&s_nmarked, 1)] = e;
     __syncthreads();
     // 2. recompute the marked rows exactly (one wave each), then rank again
-    for (int q = wave; q < s_nmarked; q += 4) {
+    const int nm = s_nmarked;
+    for (int q = wave; q < nm; q += 4) {
         const int e = s_marked[q];
         const double v = moe_ref_row(a.type, a.W + (unsigned long long)e * a.row_bytes, a.H, a.bs, a.bpb, x);
-        if (lane == 0) { s_l[e] = v; s_b[e] = 0.0; }
+        if (lane == 0) { s_l[e] = isnan(v) ? -INFINITY : v; s_b[e] = 0.0; }
     }
     __syncthreads();
-    select_top(k);
+    if (nm > 0) rank_top(k);
 
-    // 3. softmax of the logits (max-subtracted, summed in expert order), the
-    //    chosen probabilities, renormalisation and scale (thread 0; E and k are small)
+    // 3. softmax: peak, exp(l - peak) summed (tree order; the reference sums
+    //    left to right, which moves the weights by fp64 rounding only), the
+    //    chosen probabilities, renormalisation and scale
+    double peak = -INFINITY;
+    for (int e = tid; e < E; e += 256) peak = fmax(peak, s_l[e]);
+    for (int off = 32; off > 0; off >>= 1) peak = fmax(peak, __shfl_xor(peak, off, 64));
+    if (lane == 0) s_red[wave] = peak;
+    __syncthreads();
+    peak = fmax(fmax(s_red[0], s_red[1]), fmax(s_red[2], s_red[3]));
+    __syncthreads();
+    double tot = 0.0;
+    for (int e = tid; e < E; e += 256) tot += exp(s_l[e] - peak);
+    for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off, 64);
+    if (lane == 0) s_red[wave] = tot;
+    __syncthreads();
+    const double total = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
     if (tid == 0) {
-        double peak = s_l[0];
-        for (int e = 1; e < E; ++e) if (s_l[e] > peak) peak = s_l[e];
-        double total = 0.0;
-        for (int e = 0; e < E; ++e) total += exp(s_l[e] - peak);
         double w[kMoeMaxK];
-        for (int s = 0; s < k; ++s) {
-            const int e = s_top[s];
-            w[s] = total <= 0.0 ? 1.0 / (double)E : exp(s_l[e] - peak) / total;
+        for (int q = 0; q < k; ++q) {
+            const int e = s_top[q];
+            w[q] = total <= 0.0 ? 1.0 / (double)E : exp(s_l[e] - peak) / total;
         }
         if (a.norm_topk) {
             double tk = 0.0;
-            for (int s = 0; s < k; ++s) tk += w[s];
-            if (tk > 0) for (int s = 0; s < k; ++s) w[s] = w[s] / tk;
+            for (int q = 0; q < k; ++q) tk += w[q];
+            if (tk > 0) for (int q = 0; q < k; ++q) w[q] = w[q] / tk;
         }
-        if (a.scale != 1.0) for (int s = 0; s < k; ++s) w[s] = w[s] * a.scale;
-        for (int s = 0; s < k; ++s) {
-            const unsigned long long o = (unsigned long long)t * k + s;
-            a.ids[o] = s_top[s];
-            a.wts[o] = w[s];
-            if (a.ids_out) a.ids_out[o] = s_top[s];
-            if (a.wts_out) a.wts_out[o] = (float)w[s];
+        if (a.scale != 1.0) for (int q = 0; q < k; ++q) w[q] = w[q] * a.scale;
+        for (int q = 0; q < k; ++q) {
+            const unsigned long long o = (unsigned long long)t * k + q;
+            a.ids[o] = s_top[q];
+            a.wts[o] = w[q];
+            if (a.ids_out) a.ids_out[o] = s_top[q];
+            if (a.wts_out) a.wts_out[o] = (float)w[q];
         }
         __threadfence();
         s_last = (atomicAdd(a.arrive, 1u) == (unsigned)a.batch - 1);
@@ -234,38 +238,44 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     __syncthreads();
     if (!s_last) return;
 
-    // 4. plan (last workgroup): bucket the (token, slot) pairs by expert, in
-    //    token order, padded to chunks of MB
+    // 4. plan (last workgroup): bucket the (token, slot) pairs by expert,
+    //    padded to chunks of MB.  The order inside a bucket does not matter:
+    //    each pair's results are computed independently of its chunk mates.
     const MoePlan& p = a.plan;
-    for (int e = tid; e < E; e += 256) p.cnt[e] = 0;
+    int* s_cnt = s_marked;  // reuse: E ints
+    for (int e = tid; e < E; e += 256) s_cnt[e] = 0;
     __syncthreads();
     const int npairs = a.batch * k;
+    for (int q = tid; q < npairs; q += 256) atomicAdd(&s_cnt[a.ids[q]], 1);
+    __syncthreads();
     if (tid == 0) {
-        // sequential: npairs <= 64 * 32 in practice; keeps the token order deterministic
-        for (int q = 0; q < npairs; ++q) p.cnt[a.ids[q]] += 1;
         int po = 0, co = 0;
         for (int e = 0; e < E; ++e) {
             p.poff[e] = po;
+            s_poff[e] = po;
             p.coff[e] = co;
-            const int nc = (p.cnt[e] + a.MB - 1) / a.MB;
+            p.cnt[e] = s_cnt[e];
+            const int nc = (s_cnt[e] + a.MB - 1) / a.MB;
+            s_cnt[e] = po;  // becomes the fill cursor
             co += nc;
             po += nc * a.MB;
         }
         p.poff[E] = po;
+        s_poff[E] = po;
         p.coff[E] = co;
         p.totals[0] = po;
         p.totals[1] = co;
-        for (int e = 0; e < E; ++e) p.cnt[e] = 0;
-        for (int q = 0; q < npairs; ++q) {
-            const int e = a.ids[q];
-            const int slot = p.poff[e] + p.cnt[e]++;
-            p.pair_tok[slot] = q / k;
-            p.pos[q] = slot;
-        }
-        for (int e = 0; e < E; ++e)
-            for (int q = p.poff[e] + p.cnt[e]; q < p.poff[e + 1]; ++q) p.pair_tok[q] = -1;
-        a.arrive[0] = 0u;
     }
+    __syncthreads();
+    for (int q = tid; q < npairs; q += 256) {
+        const int slot = atomicAdd(&s_cnt[a.ids[q]], 1);
+        p.pair_tok[slot] = q / k;
+        p.pos[q] = slot;
+    }
+    __syncthreads();
+    for (int e = tid; e < E; e += 256)
+        for (int q = s_cnt[e]; q < s_poff[e + 1]; ++q) p.pair_tok[q] = -1;
+    if (tid == 0) a.arrive[0] = 0u;
 }
 
 // ---------------------------------------------------------------- gather, swiglu, combine
@@ -452,7 +462,7 @@ static hipError_t moe_mv_launch_t(MoeMvArgs a, bool al, hipStream_t s) {
         max_cols = a.m[j].cols > max_cols ? a.m[j].cols : max_cols;
     }
     constexpr bool AQ = Geo<T>::bpb % 4 == 0;
-    if constexpr (Geo<T>::bs > 1 && MB <= 2) {
+    if constexpr (Geo<T>::bs > 1) {
         if (use_xl<T, MB, false>(max_cols)) {
             const size_t lds = lds_bytes<T, MB, false>(max_cols, true);
             return al && AQ ? moe_mv_launch_x<T, MB, AQ, true>(a, lds, s) : moe_mv_launch_x<T, MB, false, true>(a, lds, s);
@@ -527,7 +537,7 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     layout(cw, &logits, &mags, &ids, &wts, &plan, &xg, &g, &u, &act, &yd);
 
     // 1. router
-    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)((E + 3) / 4), (unsigned)batch), dim3(256), 0, stream,
+    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)E, (unsigned)batch), dim3(64), 0, stream,
                        L.router_type, static_cast<const uint8_t*>(L.router), (unsigned long long)rr, (int)E, (int)H,
                        gr.bs, gr.bpb, X, (unsigned long long)ldx, logits, mags);
     if (hipGetLastError() != hipSuccess) return -4;

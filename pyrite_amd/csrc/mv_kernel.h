@@ -355,7 +355,7 @@ static size_t lds_bytes(int max_cols, bool xl) {
 }
 template <int T, int B, bool BD>
 static bool use_xl(int max_cols) {
-    return Geo<T>::bs > 1 && B <= 2 && lds_bytes<T, B, BD>(max_cols, true) <= 65536;
+    return Geo<T>::bs > 1 && lds_bytes<T, B, BD>(max_cols, true) <= 65536;
 }
 
 // Slot shape of one matrix (rows per slot R, lanes per row), a function of
@@ -415,7 +415,7 @@ template <int T, int B, int R, bool AL, bool BD>
 static hipError_t launch_group_rx(const MvGroup& g, hipStream_t stream, LaunchEvents ev) {
     int max_cols = 0;
     for (int i = 0; i < g.n; ++i) max_cols = g.d[i].cols > max_cols ? g.d[i].cols : max_cols;
-    if constexpr (Geo<T>::bs > 1 && B <= 2) {
+    if constexpr (Geo<T>::bs > 1) {
         if (use_xl<T, B, BD>(max_cols))
             return launch_group_r<T, B, R, AL, true, BD>(g, lds_bytes<T, B, BD>(max_cols, true), stream, ev);
     }
