@@ -187,6 +187,39 @@ __device__ __forceinline__ uint32_t spread4(uint32_t v) {
     return ((v & 0xFu) * 0x00204081u) & 0x01010101u;
 }
 
+// ---------------------------------------------------------------- cross-workgroup hand-off
+// A "last workgroup to arrive" step reads values that other workgroups of the
+// same launch wrote.  An agent-scope fence would make them visible, but on
+// gfx950 it writes back the whole L2 of the XCD (buffer_wbl2), which costs
+// microseconds per call.  Instead the shared values are stored and loaded as
+// agent-scope relaxed atomics (device-coherent accesses that do not leave
+// stale copies in a per-XCD L2), and a workgroup increments the arrival
+// counter only after its own stores have completed (s_waitcnt 0).  The reader
+// runs only after observing the final count.  Nothing spins: a workgroup that
+// is not last simply exits.
+template <typename V>
+__device__ __forceinline__ void st_dev(V* p, V v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename V>
+__device__ __forceinline__ V ld_dev(const V* p) {
+    return __hip_atomic_load(const_cast<V*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// wait until this wave's earlier memory operations have completed
+__device__ __forceinline__ void drain_dev() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+// returns the counter's previous value; every wave that stored shared values
+// must drain_dev() before the barrier that precedes this call
+__device__ __forceinline__ unsigned arrive_dev(unsigned* counter) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---------------------------------------------------------------- lane sums
 // GFX9 DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1]
 // (lane ^ 2), row_half_mirror (lane i <-> 7 - i inside 8), row_mirror

@@ -52,6 +52,7 @@ struct LmArgs {
     double* ws_L;            // [batch][kLmWgs]
     int* ws_cnt;             // [batch][kLmWgs]  (-1: non-finite seen)
     int* ws_cand;            // [batch][kLmWgs][kLmCand]
+    double* ws_candv;        // [batch][kLmWgs][kLmCand]: y + B of each listed row
     unsigned int* ws_arrive; // [batch]
 };
 
@@ -147,31 +148,33 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
 
     // pass 2: rows that can still beat L_w (a superset of the token's candidates in this range)
     int* cand = a.ws_cand + ((unsigned long long)t * kLmWgs + w) * kLmCand;
+    double* candv = a.ws_candv + ((unsigned long long)t * kLmWgs + w) * kLmCand;
     if (!nf) {
         const double lc = lmax - fabs(lmax) * 0x1p-50;
         for (int r = r0 + tid; r < r1; r += 256) {
-            if (hi(r) >= lc) {
+            const double h = hi(r);
+            if (h >= lc) {
                 const int k = atomicAdd(&s_cnt, 1);
-                if (k < kLmCand) cand[k] = r;
+                if (k < kLmCand) { st_dev(cand + k, r); st_dev(candv + k, h); }
             }
         }
     }
     __syncthreads();
     if (tid == 0) {
-        a.ws_L[(unsigned long long)t * kLmWgs + w] = lmax;
-        a.ws_cnt[(unsigned long long)t * kLmWgs + w] = nf ? -1 : s_cnt;
-        __threadfence();
-        const unsigned prev = atomicAdd(a.ws_arrive + t, 1u);
-        s_last = (prev == kLmWgs - 1);
-        if (s_last) __threadfence();
+        st_dev(a.ws_L + (unsigned long long)t * kLmWgs + w, lmax);
+        st_dev(a.ws_cnt + (unsigned long long)t * kLmWgs + w, nf ? -1 : s_cnt);
     }
+    drain_dev();  // every wave's candidate stores have completed ...
+    __syncthreads();
+    if (tid == 0) s_last = (arrive_dev(a.ws_arrive + t) == kLmWgs - 1);  // ... before the arrival
+    __syncthreads();
     __syncthreads();
     if (!s_last) return;
 
     // ---- deciding workgroup of token t; thread k looks after workgroup k's range
     static_assert(kLmWgs == 256, "one thread per argmax workgroup");
-    const int my_cnt = a.ws_cnt[(unsigned long long)t * kLmWgs + tid];
-    double L = a.ws_L[(unsigned long long)t * kLmWgs + tid];
+    const int my_cnt = ld_dev(a.ws_cnt + (unsigned long long)t * kLmWgs + tid);
+    double L = ld_dev(a.ws_L + (unsigned long long)t * kLmWgs + tid);
     int any_nf = my_cnt < 0;
     for (int off = 32; off > 0; off >>= 1) {
         L = fmax(L, __shfl_xor(L, off, 64));
@@ -195,19 +198,7 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
             if (lane == 0) a.ids[t] = bi;
         }
         __syncthreads();
-        if (tid == 0) a.ws_arrive[t] = 0u;
-        return;
-    }
-
-    // All-zero activations: every reference logit is +-0, which compare
-    // equal, so the first row wins.
-    int nz = 0;
-    for (int c = tid; c < a.cols; c += 256) nz |= (x[c] != 0.f);
-    for (int off = 32; off > 0; off >>= 1) nz |= __shfl_xor(nz, off, 64);
-    if (lane == 0) s_flag[wave] = nz;
-    __syncthreads();
-    if (!(s_flag[0] | s_flag[1] | s_flag[2] | s_flag[3])) {
-        if (tid == 0) { a.ids[t] = 0; a.ws_arrive[t] = 0u; }
+        if (tid == 0) st_dev(a.ws_arrive + t, 0u);
         return;
     }
 
@@ -218,24 +209,38 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
     __syncthreads();
     double bv = -INFINITY;
     int br = 0x7FFFFFFF;
-    auto consider = [&](int r) {
-        if (hi(r) < Lc) return;
+    auto consider = [&](int r, double h) {
+        if (h < Lc) return;
         s_one = r;  // any candidate; used only when there is exactly one
         const int q = atomicAdd(&s_nref, 1);
         if (q < kLmKept) s_kept[q] = r;
     };
     if (my_cnt > 0 && my_cnt <= kLmCand) {
-        const int* lst = a.ws_cand + ((unsigned long long)t * kLmWgs + tid) * kLmCand;
-        for (int q = 0; q < my_cnt; ++q) consider(lst[q]);
+        const unsigned long long base = ((unsigned long long)t * kLmWgs + tid) * kLmCand;
+        int rs[kLmCand];
+        double hs[kLmCand];
+        for (int q = 0; q < my_cnt; ++q) { rs[q] = ld_dev(a.ws_cand + base + q); hs[q] = ld_dev(a.ws_candv + base + q); }
+        for (int q = 0; q < my_cnt; ++q) consider(rs[q], hs[q]);
     } else if (my_cnt > kLmCand) {
         int q0, q1;
         range(tid, q0, q1);
-        for (int r = q0; r < q1; ++r) consider(r);
+        for (int r = q0; r < q1; ++r) consider(r, hi(r));
     }
     __syncthreads();
     const int nref = s_nref;
     if (nref == 1) {
-        if (tid == 0) { a.ids[t] = s_one; a.ws_arrive[t] = 0u; }
+        if (tid == 0) { a.ids[t] = s_one; st_dev(a.ws_arrive + t, 0u); }
+        return;
+    }
+    // All-zero activations: every reference logit is +-0, which compare
+    // equal, so the first row wins.
+    int nz = 0;
+    for (int c = tid; c < a.cols; c += 256) nz |= (x[c] != 0.f);
+    for (int off = 32; off > 0; off >>= 1) nz |= __shfl_xor(nz, off, 64);
+    if (lane == 0) s_flag[wave] = nz;
+    __syncthreads();
+    if (!(s_flag[0] | s_flag[1] | s_flag[2] | s_flag[3])) {
+        if (tid == 0) { a.ids[t] = 0; st_dev(a.ws_arrive + t, 0u); }
         return;
     }
     for (int q = wave; q < (nref < kLmKept ? nref : kLmKept); q += 4) {
@@ -254,7 +259,7 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
     block_best(bv, br, s_bv, s_br);
     if (tid == 0) {
         a.ids[t] = br == 0x7FFFFFFF ? -1 : br;
-        a.ws_arrive[t] = 0u;
+        st_dev(a.ws_arrive + t, 0u);
     }
 }
 
@@ -266,6 +271,7 @@ struct LmWorkspace {
     double* L = nullptr;
     int* cnt = nullptr;
     int* cand = nullptr;
+    double* candv = nullptr;
     unsigned int* arrive = nullptr;
     size_t tokens = 0;
 };
@@ -296,11 +302,13 @@ static int lm_workspace(size_t bnd_floats, size_t tokens, hipStream_t stream, Lm
         if (w.L) (void)hipFree(w.L);
         if (w.cnt) (void)hipFree(w.cnt);
         if (w.cand) (void)hipFree(w.cand);
+        if (w.candv) (void)hipFree(w.candv);
         if (w.arrive) (void)hipFree(w.arrive);
-        w.L = nullptr; w.cnt = nullptr; w.cand = nullptr; w.arrive = nullptr; w.tokens = 0;
+        w.L = nullptr; w.cnt = nullptr; w.cand = nullptr; w.candv = nullptr; w.arrive = nullptr; w.tokens = 0;
         if (hipMalloc(&w.L, tokens * kLmWgs * sizeof(double)) != hipSuccess) return -4;
         if (hipMalloc(&w.cnt, tokens * kLmWgs * sizeof(int)) != hipSuccess) return -4;
         if (hipMalloc(&w.cand, tokens * kLmWgs * kLmCand * sizeof(int)) != hipSuccess) return -4;
+        if (hipMalloc(&w.candv, tokens * kLmWgs * kLmCand * sizeof(double)) != hipSuccess) return -4;
         if (hipMalloc(&w.arrive, tokens * sizeof(unsigned int)) != hipSuccess) return -4;
         if (hipMemset(w.arrive, 0, tokens * sizeof(unsigned int)) != hipSuccess) return -4;
         if (hipDeviceSynchronize() != hipSuccess) return -4;
@@ -367,6 +375,7 @@ int lm_head_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t
     a.ws_L = ws->L;
     a.ws_cnt = ws->cnt;
     a.ws_cand = ws->cand;
+    a.ws_candv = ws->candv;
     a.ws_arrive = ws->arrive;
     if (batch > 65535) return -2;
     hipLaunchKernelGGL(lm_argmax_kernel, dim3(kLmWgs, (unsigned)batch), dim3(256), 0, stream, a);

@@ -160,6 +160,7 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
         for (int e = tid; e < E; e += 256) {
             const double le = s_l[e];
             int r = 0;
+#pragma unroll 8
             for (int j = 0; j < E; ++j) r += rank_before(s_l[j], j, le, e);
             if (r < n) s_top[r] = e;
         }
@@ -226,14 +227,12 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
         if (a.scale != 1.0) for (int q = 0; q < k; ++q) w[q] = w[q] * a.scale;
         for (int q = 0; q < k; ++q) {
             const unsigned long long o = (unsigned long long)t * k + q;
-            a.ids[o] = s_top[q];
+            st_dev(a.ids + o, s_top[q]);
             a.wts[o] = w[q];
             if (a.ids_out) a.ids_out[o] = s_top[q];
             if (a.wts_out) a.wts_out[o] = (float)w[q];
         }
-        __threadfence();
-        s_last = (atomicAdd(a.arrive, 1u) == (unsigned)a.batch - 1);
-        if (s_last) __threadfence();
+        s_last = (arrive_dev(a.arrive) == (unsigned)a.batch - 1);
     }
     __syncthreads();
     if (!s_last) return;
@@ -246,36 +245,67 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     for (int e = tid; e < E; e += 256) s_cnt[e] = 0;
     __syncthreads();
     const int npairs = a.batch * k;
-    for (int q = tid; q < npairs; q += 256) atomicAdd(&s_cnt[a.ids[q]], 1);
+    for (int q = tid; q < npairs; q += 256) atomicAdd(&s_cnt[ld_dev(a.ids + q)], 1);
     __syncthreads();
-    if (tid == 0) {
-        int po = 0, co = 0;
-        for (int e = 0; e < E; ++e) {
-            p.poff[e] = po;
-            s_poff[e] = po;
-            p.coff[e] = co;
-            p.cnt[e] = s_cnt[e];
-            const int nc = (s_cnt[e] + a.MB - 1) / a.MB;
-            s_cnt[e] = po;  // becomes the fill cursor
-            co += nc;
-            po += nc * a.MB;
+    // exclusive prefix sums over experts of padded pairs and chunks: each
+    // thread scans 4 consecutive experts, then the 256 thread totals
+    {
+        const int e0 = tid * 4;
+        int cp[4], cc[4], sp = 0, sc = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = e0 + j;
+            const int n = e < E ? s_cnt[e] : 0;
+            const int nc = (n + a.MB - 1) / a.MB;
+            cp[j] = sp;
+            cc[j] = sc;
+            sp += nc * a.MB;
+            sc += nc;
         }
-        p.poff[E] = po;
-        s_poff[E] = po;
-        p.coff[E] = co;
-        p.totals[0] = po;
-        p.totals[1] = co;
+        // inclusive scan of (sp, sc) across the wave
+        int ip = sp, ic = sc;
+        for (int off = 1; off < 64; off <<= 1) {
+            const int up = __shfl_up(ip, off, 64), uc = __shfl_up(ic, off, 64);
+            if (lane >= off) { ip += up; ic += uc; }
+        }
+        __shared__ int s_wp[4], s_wc[4];
+        if (lane == 63) { s_wp[wave] = ip; s_wc[wave] = ic; }
+        __syncthreads();
+        int bp = 0, bc = 0;
+        for (int w2 = 0; w2 < wave; ++w2) { bp += s_wp[w2]; bc += s_wc[w2]; }
+        bp += ip - sp;  // exclusive prefix of this thread
+        bc += ic - sc;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = e0 + j;
+            if (e < E) {
+                p.poff[e] = bp + cp[j];
+                s_poff[e] = bp + cp[j];
+                p.coff[e] = bc + cc[j];
+                p.cnt[e] = s_cnt[e];
+            }
+        }
+        if (tid == 255) {
+            const int tp = bp + sp, tc = bc + sc;
+            p.poff[E] = tp;
+            s_poff[E] = tp;
+            p.coff[E] = tc;
+            p.totals[0] = tp;
+            p.totals[1] = tc;
+        }
+        __syncthreads();
+        for (int e = tid; e < E; e += 256) s_cnt[e] = s_poff[e];  // fill cursors
+        __syncthreads();
     }
-    __syncthreads();
     for (int q = tid; q < npairs; q += 256) {
-        const int slot = atomicAdd(&s_cnt[a.ids[q]], 1);
+        const int slot = atomicAdd(&s_cnt[ld_dev(a.ids + q)], 1);
         p.pair_tok[slot] = q / k;
         p.pos[q] = slot;
     }
     __syncthreads();
     for (int e = tid; e < E; e += 256)
         for (int q = s_cnt[e]; q < s_poff[e + 1]; ++q) p.pair_tok[q] = -1;
-    if (tid == 0) a.arrive[0] = 0u;
+    if (tid == 0) st_dev(a.arrive, 0u);
 }
 
 // ---------------------------------------------------------------- gather, swiglu, combine

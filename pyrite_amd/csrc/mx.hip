@@ -673,23 +673,18 @@ __global__ __launch_bounds__(256) void mx_kernel(const MxGroup grp) {
         } else {
             // split K: publish this part; the last part to arrive sums all parts
             // in part order (deterministic) and writes y, then re-arms the
-            // counter.  One device-scope release (and acquire) per task, by
-            // thread 0, after the workgroup's stores have reached L2.
+            // counter (device-coherent hand-off, see st_dev / arrive_dev).
             float* pt = d.part + ((size_t)kp * d.tiles + tile) * 256;
-            pt[trow * 8 + t] = sum;
+            st_dev(pt + trow * 8 + t, sum);
+            drain_dev();
             __syncthreads();
-            if (tid == 0) {
-                __threadfence();
-                const bool last = atomicAdd(&d.counters[tile], 1u) == (unsigned)(d.ksplit - 1);
-                if (last) __threadfence();
-                last_flag = last;
-            }
+            if (tid == 0) last_flag = arrive_dev(&d.counters[tile]) == (unsigned)(d.ksplit - 1);
             __syncthreads();
             if (last_flag) {
                 float tot = 0.f;
-                for (int k = 0; k < d.ksplit; ++k) tot += d.part[((size_t)k * d.tiles + tile) * 256 + trow * 8 + t];
+                for (int k = 0; k < d.ksplit; ++k) tot += ld_dev(d.part + ((size_t)k * d.tiles + tile) * 256 + trow * 8 + t);
                 if (t < d.batch && row < rows) d.Y[t * d.ldy + row] = tot;
-                if (tid == 0) d.counters[tile] = 0u;
+                if (tid == 0) st_dev(&d.counters[tile], 0u);
             }
         }
         lds_barrier();
