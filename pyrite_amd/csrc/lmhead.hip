@@ -217,10 +217,7 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
     };
     if (my_cnt > 0 && my_cnt <= kLmCand) {
         const unsigned long long base = ((unsigned long long)t * kLmWgs + tid) * kLmCand;
-        int rs[kLmCand];
-        double hs[kLmCand];
-        for (int q = 0; q < my_cnt; ++q) { rs[q] = ld_dev(a.ws_cand + base + q); hs[q] = ld_dev(a.ws_candv + base + q); }
-        for (int q = 0; q < my_cnt; ++q) consider(rs[q], hs[q]);
+        for (int q = 0; q < my_cnt; ++q) consider(ld_dev(a.ws_cand + base + q), ld_dev(a.ws_candv + base + q));
     } else if (my_cnt > kLmCand) {
         int q0, q1;
         range(tid, q0, q1);

@@ -17,11 +17,14 @@
 //                       the reference's own order), softmax, top-k, weights;
 //                       the last token's workgroup buckets (token, slot)
 //                       pairs by expert into padded chunks of MB tokens
-//   moe_gather_kernel   activations of each bucket, zero padding
 //   moe_mv_kernel       gate and up (one launch), then down: persistent
 //                       workgroups walk (matrix, chunk, row tile) items and run
-//                       the VALU matvec body on each, weights read once per chunk
-//   moe_swiglu_kernel   act = silu(gate) * up (fp64 inside)
+//                       the VALU matvec body on each, weights read once per
+//                       chunk; the gate/up launch gathers each chunk's tokens
+//                       while staging them, the down launch applies
+//                       silu(gate) * up (fp64 inside) while staging
+//   moe_gather_kernel,  used instead when the staged activations would not
+//   moe_swiglu_kernel   fit the LDS budget
 //   moe_combine_kernel  out = sum of w * down-out in slot order (fp64 inside)
 #include "dequant.h"
 #include "mv_kernel.h"
@@ -213,24 +216,25 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     if (lane == 0) s_red[wave] = tot;
     __syncthreads();
     const double total = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    __shared__ double s_w[kMoeMaxK];
+    if (tid < k) {
+        const int e = s_top[tid];
+        s_w[tid] = total <= 0.0 ? 1.0 / (double)E : exp(s_l[e] - peak) / total;
+    }
+    __syncthreads();
     if (tid == 0) {
-        double w[kMoeMaxK];
+        double tk = 0.0;
+        if (a.norm_topk)
+            for (int q = 0; q < k; ++q) tk += s_w[q];
         for (int q = 0; q < k; ++q) {
-            const int e = s_top[q];
-            w[q] = total <= 0.0 ? 1.0 / (double)E : exp(s_l[e] - peak) / total;
-        }
-        if (a.norm_topk) {
-            double tk = 0.0;
-            for (int q = 0; q < k; ++q) tk += w[q];
-            if (tk > 0) for (int q = 0; q < k; ++q) w[q] = w[q] / tk;
-        }
-        if (a.scale != 1.0) for (int q = 0; q < k; ++q) w[q] = w[q] * a.scale;
-        for (int q = 0; q < k; ++q) {
+            double w = s_w[q];
+            if (a.norm_topk && tk > 0) w = w / tk;
+            if (a.scale != 1.0) w = w * a.scale;
             const unsigned long long o = (unsigned long long)t * k + q;
             st_dev(a.ids + o, s_top[q]);
-            a.wts[o] = w[q];
+            a.wts[o] = w;
             if (a.ids_out) a.ids_out[o] = s_top[q];
-            if (a.wts_out) a.wts_out[o] = (float)w[q];
+            if (a.wts_out) a.wts_out[o] = (float)w;
         }
         s_last = (arrive_dev(a.arrive) == (unsigned)a.batch - 1);
     }
@@ -355,7 +359,8 @@ struct MoeMat {
     const uint8_t* W;           // stacked [E][rows][row_bytes]
     unsigned long long slice;   // bytes per expert
     unsigned long long row_bytes;
-    const float* X;             // [padded pairs][cols]
+    const float* X;             // [padded pairs][cols] (XGather: the caller's [batch][ldx] tokens)
+    const float* X2;            // XSwiglu: up rows [padded pairs][cols]
     float* Y;                   // [padded pairs][rows]
     int rows, cols, lpr_log2;
 };
@@ -368,11 +373,13 @@ struct MoeMvArgs {
     const int* poff;            // [E + 1] padded pair offsets
     const int* totals;          // [1]: chunks
     int E;
+    const int* pair_tok;        // XGather: token of each padded pair
+    unsigned long long ldx_tokens;
 };
 
 // Item i -> matrix (i / per_matrix), chunk, row tile; chunk -> expert by
 // binary search over the chunk offsets.
-template <int T, int MB, bool AL, bool XL>
+template <int T, int MB, bool AL, bool XL, class XS>
 __global__ __launch_bounds__(kMvThreads) void moe_mv_kernel(const MoeMvArgs a) {
     extern __shared__ float smem[];
     const int chunks = a.totals[1];
@@ -401,8 +408,16 @@ __global__ __launch_bounds__(kMvThreads) void moe_mv_kernel(const MoeMvArgs a) {
         MvDesc d;
         d.W = m.W + (unsigned long long)e * m.slice + (unsigned long long)row0 * m.row_bytes;
         d.row_bytes = m.row_bytes;
-        d.X = m.X + (unsigned long long)pair0 * m.cols;
-        d.ldx = m.cols;
+        if constexpr (std::is_same<XS, XGather>::value) {
+            d.X = m.X;  // the caller's tokens, gathered through pair_tok
+            d.ldx = a.ldx_tokens;
+            d.xrow = a.pair_tok + pair0;
+        } else {
+            d.X = m.X + (unsigned long long)pair0 * m.cols;
+            d.ldx = m.cols;
+            d.xrow = nullptr;
+        }
+        d.X2 = std::is_same<XS, XSwiglu>::value ? m.X2 + (unsigned long long)pair0 * m.cols : nullptr;
         d.Y = m.Y + (unsigned long long)pair0 * m.rows + row0;
         d.ldy = m.rows;
         d.rows = m.rows - row0 < a.tile ? m.rows - row0 : a.tile;
@@ -413,7 +428,7 @@ __global__ __launch_bounds__(kMvThreads) void moe_mv_kernel(const MoeMvArgs a) {
         d.pad = 0;
         d.Bnd = nullptr;
         __syncthreads();  // the previous item's waves are done with LDS
-        mv_body<T, MB, 1, AL, XL, false>(d, 0, smem);
+        mv_body<T, MB, 1, AL, XL, false, XS>(d, 0, smem);
     }
 }
 
@@ -467,12 +482,12 @@ struct Carver {
     }
 };
 
-template <int T, int MB, bool AL, bool XL>
+template <int T, int MB, bool AL, bool XL, class XS>
 static hipError_t moe_mv_launch_x(const MoeMvArgs& a, size_t lds, hipStream_t s) {
     const DevInfo& di = dev_info();
     static const int per_cu = [] {
         int v = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, moe_mv_kernel<T, MB, AL, XL>, kMvThreads, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, moe_mv_kernel<T, MB, AL, XL, XS>, kMvThreads, 0) != hipSuccess ||
             v < 1)
             v = 1;
         return v;
@@ -480,12 +495,15 @@ static hipError_t moe_mv_launch_x(const MoeMvArgs& a, size_t lds, hipStream_t s)
     long long pc = per_cu;
     if (lds > 0 && (long long)(di.lds_per_cu / lds) < pc) pc = (long long)(di.lds_per_cu / lds);
     if (pc < 1) pc = 1;
-    hipLaunchKernelGGL((moe_mv_kernel<T, MB, AL, XL>), dim3((unsigned)(pc * di.cus)), dim3(kMvThreads), lds, s, a);
+    hipLaunchKernelGGL((moe_mv_kernel<T, MB, AL, XL, XS>), dim3((unsigned)(pc * di.cus)), dim3(kMvThreads), lds, s, a);
     return hipGetLastError();
 }
 
+// mode 0: activations already gathered / activated (XDirect); 1: gather the
+// caller's tokens (XGather); 2: SwiGLU of the gate and up rows (XSwiglu).
+// Modes 1 and 2 need the activations staged in LDS (moe_fused_ok).
 template <int T, int MB>
-static hipError_t moe_mv_launch_t(MoeMvArgs a, bool al, hipStream_t s) {
+static hipError_t moe_mv_launch_t(MoeMvArgs a, bool al, int mode, hipStream_t s) {
     int max_cols = 0;
     for (int j = 0; j < a.nm; ++j) {
         a.m[j].lpr_log2 = plan_lpr(units_per_row<T>(a.m[j].cols));
@@ -495,27 +513,48 @@ static hipError_t moe_mv_launch_t(MoeMvArgs a, bool al, hipStream_t s) {
     if constexpr (Geo<T>::bs > 1) {
         if (use_xl<T, MB, false>(max_cols)) {
             const size_t lds = lds_bytes<T, MB, false>(max_cols, true);
-            return al && AQ ? moe_mv_launch_x<T, MB, AQ, true>(a, lds, s) : moe_mv_launch_x<T, MB, false, true>(a, lds, s);
+            if (mode == 1)
+                return al && AQ ? moe_mv_launch_x<T, MB, AQ, true, XGather>(a, lds, s)
+                                : moe_mv_launch_x<T, MB, false, true, XGather>(a, lds, s);
+            if (mode == 2)
+                return al && AQ ? moe_mv_launch_x<T, MB, AQ, true, XSwiglu>(a, lds, s)
+                                : moe_mv_launch_x<T, MB, false, true, XSwiglu>(a, lds, s);
+            return al && AQ ? moe_mv_launch_x<T, MB, AQ, true, XDirect>(a, lds, s)
+                            : moe_mv_launch_x<T, MB, false, true, XDirect>(a, lds, s);
         }
     }
+    if (mode != 0) return hipErrorInvalidValue;
     const size_t lds = lds_bytes<T, MB, false>(max_cols, false);
-    return al && AQ ? moe_mv_launch_x<T, MB, AQ, false>(a, lds, s) : moe_mv_launch_x<T, MB, false, false>(a, lds, s);
+    return al && AQ ? moe_mv_launch_x<T, MB, AQ, false, XDirect>(a, lds, s)
+                    : moe_mv_launch_x<T, MB, false, false, XDirect>(a, lds, s);
 }
 
-static hipError_t moe_mv_launch(int type, int MB, const MoeMvArgs& a, bool al, hipStream_t s) {
+static hipError_t moe_mv_launch(int type, int MB, const MoeMvArgs& a, bool al, int mode, hipStream_t s) {
 #define PYRITE_CASE(T)                                                 \
     case T:                                                          \
         switch (MB) {                                                \
-        case 1: return moe_mv_launch_t<T, 1>(a, al, s);              \
-        case 2: return moe_mv_launch_t<T, 2>(a, al, s);              \
-        case 4: return moe_mv_launch_t<T, 4>(a, al, s);              \
-        default: return moe_mv_launch_t<T, 8>(a, al, s);             \
+        case 1: return moe_mv_launch_t<T, 1>(a, al, mode, s);        \
+        case 2: return moe_mv_launch_t<T, 2>(a, al, mode, s);        \
+        case 4: return moe_mv_launch_t<T, 4>(a, al, mode, s);        \
+        default: return moe_mv_launch_t<T, 8>(a, al, mode, s);       \
         }
     switch (type) {
         PYRITE_FOR_EACH_TYPE(PYRITE_CASE)
     default: return hipErrorInvalidValue;
     }
 #undef PYRITE_CASE
+}
+
+// Whether the fused gather / SwiGLU staging applies: quantized types whose
+// staged activations fit the LDS budget.
+static bool moe_fused_ok(int type, int MB, size_t cols) {
+    const TypeGeo g = type_geo(type);
+    if (g.bs == 1) return false;
+    const int padi = (type == T_Q6_K || type == T_Q2_K || type == T_Q3_K) ? 128
+                     : (type == T_Q4_K || type == T_Q5_K || type == T_IQ4_XS) ? 64 : 32;
+    const size_t n16r = ((size_t)MB * (cols / 16) + 3) & ~size_t(3);
+    const size_t bytes = n16r * 4 + (size_t)MB * (cols + cols / padi * 4) * 4;
+    return bytes <= 65536;
 }
 
 int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, size_t ldo, int* ids_out,
@@ -603,11 +642,16 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     ra.plan = plan;
     hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)batch), dim3(256), 0, stream, ra);
     if (hipGetLastError() != hipSuccess) return -4;
-    // 3. gather
-    const unsigned gblocks = (unsigned)(max_pairs < 4096 ? max_pairs : 4096);
-    hipLaunchKernelGGL(moe_gather_kernel, dim3(gblocks), dim3(256), 0, stream, X, (unsigned long long)ldx, (int)H,
-                       plan.pair_tok, plan.totals, (int)max_pairs, xg);
-    if (hipGetLastError() != hipSuccess) return -4;
+    // 3. gather (unless the gate/up launch gathers while staging)
+    const bool x16 = ((reinterpret_cast<uintptr_t>(X) & 15u) == 0) && (ldx % 4 == 0);
+    const bool fuse_in = x16 && moe_fused_ok(L.gate_type, MB, H) && moe_fused_ok(L.up_type, MB, H);
+    const bool fuse_act = moe_fused_ok(L.down_type, MB, I);
+    if (!fuse_in) {
+        const unsigned gblocks = (unsigned)(max_pairs < 4096 ? max_pairs : 4096);
+        hipLaunchKernelGGL(moe_gather_kernel, dim3(gblocks), dim3(256), 0, stream, X, (unsigned long long)ldx,
+                           (int)H, plan.pair_tok, plan.totals, (int)max_pairs, xg);
+        if (hipGetLastError() != hipSuccess) return -4;
+    }
     // 4. gate and up
     auto tile_for = [&](size_t rows) {
         // aim for ~2048 items per launch at the worst-case chunk count
@@ -622,40 +666,49 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     ma.poff = plan.poff;
     ma.totals = plan.totals;
     ma.E = (int)E;
-    auto mat = [&](const void* W, size_t slice, const TypeGeo& tg, const float* Xs, float* Ys, size_t rows, size_t cols) {
+    ma.pair_tok = plan.pair_tok;
+    ma.ldx_tokens = ldx;
+    auto mat = [&](const void* W, size_t slice, const TypeGeo& tg, const float* Xs, const float* X2s, float* Ys,
+                   size_t rows, size_t cols) {
         MoeMat m;
         m.W = static_cast<const uint8_t*>(W);
         m.slice = slice;
         m.row_bytes = cols / tg.bs * tg.bpb;
         m.X = Xs;
+        m.X2 = X2s;
         m.Y = Ys;
         m.rows = (int)rows;
         m.cols = (int)cols;
         m.lpr_log2 = 0;
         return m;
     };
+    const float* xin = fuse_in ? X : xg;
+    const int mode_in = fuse_in ? 1 : 0;
     ma.tile = tile_for(I);
     if (L.gate_type == L.up_type) {
         ma.nm = 2;
-        ma.m[0] = mat(L.gate, gs, gg, xg, g, I, H);
-        ma.m[1] = mat(L.up, us, gu, xg, u, I, H);
-        if (moe_mv_launch(L.gate_type, MB, ma, al_gu, stream) != hipSuccess) return -4;
+        ma.m[0] = mat(L.gate, gs, gg, xin, nullptr, g, I, H);
+        ma.m[1] = mat(L.up, us, gu, xin, nullptr, u, I, H);
+        if (moe_mv_launch(L.gate_type, MB, ma, al_gu, mode_in, stream) != hipSuccess) return -4;
     } else {
         ma.nm = 1;
-        ma.m[0] = mat(L.gate, gs, gg, xg, g, I, H);
-        if (moe_mv_launch(L.gate_type, MB, ma, al_gu, stream) != hipSuccess) return -4;
-        ma.m[0] = mat(L.up, us, gu, xg, u, I, H);
-        if (moe_mv_launch(L.up_type, MB, ma, al_gu, stream) != hipSuccess) return -4;
+        ma.m[0] = mat(L.gate, gs, gg, xin, nullptr, g, I, H);
+        if (moe_mv_launch(L.gate_type, MB, ma, al_gu, mode_in, stream) != hipSuccess) return -4;
+        ma.m[0] = mat(L.up, us, gu, xin, nullptr, u, I, H);
+        if (moe_mv_launch(L.up_type, MB, ma, al_gu, mode_in, stream) != hipSuccess) return -4;
     }
-    // 5. SwiGLU
-    hipLaunchKernelGGL(moe_swiglu_kernel, dim3(1024), dim3(256), 0, stream, g, u, (int)I, plan.totals,
-                       (int)max_pairs, act);
-    if (hipGetLastError() != hipSuccess) return -4;
+    // 5. SwiGLU (unless the down launch applies it while staging)
+    if (!fuse_act) {
+        hipLaunchKernelGGL(moe_swiglu_kernel, dim3(1024), dim3(256), 0, stream, g, u, (int)I, plan.totals,
+                           (int)max_pairs, act);
+        if (hipGetLastError() != hipSuccess) return -4;
+    }
     // 6. down
     ma.nm = 1;
     ma.tile = tile_for(H);
-    ma.m[0] = mat(L.down, ds, gd, act, yd, H, I);
-    if (moe_mv_launch(L.down_type, MB, ma, (reinterpret_cast<uintptr_t>(L.down) & 3u) == 0, stream) != hipSuccess)
+    ma.m[0] = fuse_act ? mat(L.down, ds, gd, g, u, yd, H, I) : mat(L.down, ds, gd, act, nullptr, yd, H, I);
+    if (moe_mv_launch(L.down_type, MB, ma, (reinterpret_cast<uintptr_t>(L.down) & 3u) == 0, fuse_act ? 2 : 0,
+                      stream) != hipSuccess)
         return -4;
     // 7. combine
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)batch), dim3(256), 0, stream,

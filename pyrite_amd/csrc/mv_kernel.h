@@ -43,6 +43,46 @@ struct MvDesc {
     int wg_count;  // workgroups assigned; each loops over row groups wg, wg + wg_count, ...
     int pad;
     float* Bnd;    // bound pass only: per-row magnitude sums, laid out like Y
+    const int* xrow;   // XGather: token row of each batch vector (negative: zeros)
+    const float* X2;   // XSwiglu: the up-projection rows (X holds the gate rows)
+};
+
+// How a workgroup fetches 16 activations (vector b, columns 16j..16j+15)
+// when it stages them.  XDirect: row b of X.  XGather: row xrow[b] of X, or
+// zeros.  XSwiglu: silu(X[b]) * X2[b] (pyrite/tensor_ops.py:509-510: v / (1 +
+// exp(-v)) for v > -60, else 0), in fp64, rounded to fp32.
+struct XDirect {
+    __device__ __forceinline__ static void load16(const MvDesc& d, int b, int j, float4 (&v)[4]) {
+        const float* p = d.X + b * d.ldx + 16 * j;
+        v[0] = ld_x4(p); v[1] = ld_x4(p + 4); v[2] = ld_x4(p + 8); v[3] = ld_x4(p + 12);
+    }
+};
+struct XGather {
+    __device__ __forceinline__ static void load16(const MvDesc& d, int b, int j, float4 (&v)[4]) {
+        const int t = d.xrow[b];
+        if (t < 0) {
+            v[0] = v[1] = v[2] = v[3] = make_float4(0.f, 0.f, 0.f, 0.f);
+            return;
+        }
+        const float* p = d.X + (unsigned long long)t * d.ldx + 16 * j;
+        v[0] = ld_x4(p); v[1] = ld_x4(p + 4); v[2] = ld_x4(p + 8); v[3] = ld_x4(p + 12);
+    }
+};
+struct XSwiglu {
+    __device__ __forceinline__ static float f(float g, float u) {
+        const double gd = g;
+        const double s = gd > -60.0 ? gd / (1.0 + exp(-gd)) : 0.0;
+        return (float)(s * (double)u);
+    }
+    __device__ __forceinline__ static void load16(const MvDesc& d, int b, int j, float4 (&v)[4]) {
+        const float* pg = d.X + b * d.ldx + 16 * j;
+        const float* pu = d.X2 + b * d.ldx + 16 * j;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float4 g = ld_x4(pg + 4 * k), u = ld_x4(pu + 4 * k);
+            v[k] = make_float4(f(g.x, u.x), f(g.y, u.y), f(g.z, u.z), f(g.w, u.w));
+        }
+    }
 };
 
 constexpr int kMaxGroup = 16;
@@ -60,8 +100,9 @@ struct MvGroup {
 // global memory by every unit; used when B * cols fits the LDS budget.
 // BD: also accumulate each row's magnitude sum (Unit::bound, or sum |w||x| for
 // plain types) and store it to d.Bnd.
-template <int T, int B, int R, bool AL, bool XL, bool BD>
+template <int T, int B, int R, bool AL, bool XL, bool BD, class XS = XDirect>
 __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* smem) {
+    static_assert(XL || std::is_same<XS, XDirect>::value, "indirect activations need LDS staging");
     constexpr int BS = Geo<T>::bs, BPB = Geo<T>::bpb;
     const uint8_t* __restrict__ W = d.W;
     const float* __restrict__ X = d.X;
@@ -152,8 +193,9 @@ __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* sm
         lds_f* xl = xs16 + (BD ? 2 * n16r : n16r);
         for (int i = threadIdx.x; i < B * n16; i += blockDim.x) {
             const int b = i / n16, j = i - b * n16;
-            const float* p = X + b * ldx + 16 * j;
-            const float4 a = ld_x4(p), c = ld_x4(p + 4), e = ld_x4(p + 8), f = ld_x4(p + 12);
+            float4 v4[4];
+            XS::load16(d, b, j, v4);
+            const float4 a = v4[0], c = v4[1], e = v4[2], f = v4[3];
             xs16[i] = (((a.x + a.y) + (a.z + a.w)) + ((c.x + c.y) + (c.z + c.w))) +
                       (((e.x + e.y) + (e.z + e.w)) + ((f.x + f.y) + (f.z + f.w)));
             if constexpr (BD)
