@@ -236,7 +236,8 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
             if (a.ids_out) a.ids_out[o] = s_top[q];
             if (a.wts_out) a.wts_out[o] = (float)w;
         }
-        s_last = (arrive_dev(a.arrive) == (unsigned)a.batch - 1);
+        // a single token's workgroup is the last by definition (and keeps its ids in LDS)
+        s_last = a.batch == 1 ? 1 : (arrive_dev(a.arrive) == (unsigned)a.batch - 1);
     }
     __syncthreads();
     if (!s_last) return;
@@ -247,9 +248,21 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     const MoePlan& p = a.plan;
     int* s_cnt = s_marked;  // reuse: E ints
     for (int e = tid; e < E; e += 256) s_cnt[e] = 0;
-    __syncthreads();
+    // every token's ids, read once (device-coherent loads) into LDS
+    constexpr int kIdsLds = 4096;
+    __shared__ int s_ids[kIdsLds];
     const int npairs = a.batch * k;
-    for (int q = tid; q < npairs; q += 256) atomicAdd(&s_cnt[ld_dev(a.ids + q)], 1);
+    const bool ids_in_lds = npairs <= kIdsLds;
+    auto id_of = [&](int q) { return ids_in_lds ? s_ids[q] : ld_dev(a.ids + q); };
+    if (ids_in_lds) {
+        if (a.batch == 1) {
+            for (int q = tid; q < npairs; q += 256) s_ids[q] = s_top[q];
+        } else {
+            for (int q = tid; q < npairs; q += 256) s_ids[q] = ld_dev(a.ids + q);
+        }
+    }
+    __syncthreads();
+    for (int q = tid; q < npairs; q += 256) atomicAdd(&s_cnt[id_of(q)], 1);
     __syncthreads();
     // exclusive prefix sums over experts of padded pairs and chunks: each
     // thread scans 4 consecutive experts, then the 256 thread totals
@@ -302,7 +315,7 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
         __syncthreads();
     }
     for (int q = tid; q < npairs; q += 256) {
-        const int slot = atomicAdd(&s_cnt[ld_dev(a.ids + q)], 1);
+        const int slot = atomicAdd(&s_cnt[id_of(q)], 1);
         p.pair_tok[slot] = q / k;
         p.pos[q] = slot;
     }
