@@ -5,6 +5,9 @@
 
 namespace pyrite {
 
+// From this many vectors on, quantized matrices go through the GEMM kernel.
+constexpr size_t kGemmMinBatch = 64;
+
 int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, hipStream_t stream,
                         hipEvent_t start, hipEvent_t stop) {
     const TypeGeo g = type_geo(type);
@@ -15,6 +18,15 @@ int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch
         const char* v = getenv("PYRITE_MATVEC_PATH");  // "valu" forces the VALU kernels
         return (v && v[0] == 'v') ? 1 : 0;
     }();
+    // prefill-sized batches: the MFMA dequant-GEMM, one launch per matrix
+    if (g.bs > 1 && !forced && batch >= kGemmMinBatch && mx_type_supported(type)) {
+        for (size_t i = 0; i < n; ++i) {
+            const int rc = mg_launch(type, mats[i], batch, al, stream, i == 0 ? start : nullptr,
+                                     i + 1 == n ? stop : nullptr);
+            if (rc != 0) return rc;
+        }
+        return 0;
+    }
     if (g.bs > 1 && !forced && batch >= 3 && mx_type_supported(type)) {
         for (size_t done = 0; done < batch; done += 8) {
             const size_t c = batch - done < 8 ? batch - done : 8;

@@ -179,7 +179,7 @@ def test_llama_layer_shapes(torch_dev, t, rows, cols):
     _device_matvec_check(torch_dev, t, rows, cols, 1, seed=20245000 + rows)
 
 
-@pytest.mark.parametrize("batch", [1, 8])
+@pytest.mark.parametrize("batch", [1, 8, 64])
 @pytest.mark.parametrize("t", [2, 12, 14, 23, 0], ids=lambda t: TYPES[t][0])
 def test_grouped_matvec_equals_single_launches(torch_dev, t, batch):
     """pyrite_dev_matvec_grouped over mixed shapes gives, bit for bit, what one
@@ -250,12 +250,12 @@ def test_device_matvec_random_payloads(torch_dev, t, batch):
         assert_matvec_close(y[b], ref, xs[b], rowmax, f"{TYPES[t][0]} random b{b}/{batch}")
 
 
-@pytest.mark.parametrize("cols,batch", [(1024, 1), (1024, 8), (4096, 8)])
+@pytest.mark.parametrize("cols,batch", [(1024, 1), (1024, 8), (4096, 8), (1024, 64), (4096, 70)])
 @pytest.mark.parametrize("t", [12, 14, 2, 8], ids=lambda t: TYPES[t][0])
 def test_device_matvec_large_activations(torch_dev, t, cols, batch):
     """Activations beyond the fp16 range (|x| up to 3e6) are rescaled by a
     power of two per vector; with 4096 columns at batch 8 the activations are
-    staged in several LDS chunks."""
+    staged in several LDS chunks, and batches of 64 and more take the GEMM."""
     torch = torch_dev
     from pyrite_amd import device
 
@@ -272,3 +272,63 @@ def test_device_matvec_large_activations(torch_dev, t, cols, batch):
     for b in range(batch):
         ref = o.matvec(t, payload, xs[b].astype(np.float64), rows, cols)
         assert_matvec_close(y[b], ref, xs[b], rowmax, f"{TYPES[t][0]} large-x b{b}/{batch}")
+
+
+@pytest.mark.parametrize("batch", [1, 8, 64])
+@pytest.mark.parametrize("t", [12, 14, 2, 8, 23], ids=lambda t: TYPES[t][0])
+def test_device_matvec_activation_scales(torch_dev, t, batch):
+    """Each vector scaled by its own power of ten from 1e-30 to 1e30: the fp16
+    activation fragments are normalised per vector, so the error stays
+    relative to ||x|| at every scale."""
+    torch = torch_dev
+    from pyrite_amd import device
+
+    o = oracle()
+    rows, cols = 48, 2048
+    payload = _weights(t, rows, cols, 4700 + t)
+    rng = np.random.default_rng(4800 + batch)
+    scales = 10.0 ** rng.integers(-30, 31, batch)
+    scales[0] = 1e-7
+    xs = (np.stack([o.normal(4900 + b, cols) for b in range(batch)]) * scales[:, None]).astype(np.float32)
+    announce("device_matvec_scales", TYPES[t][0], rows, cols, batch)
+    y = device.matvec(t, device.upload(payload.tobytes()), torch.from_numpy(xs).cuda(), rows, cols).cpu().numpy()
+    wd = o.dequantize_rows(t, payload, rows, cols).reshape(rows, cols)
+    rowmax = np.abs(wd).max(axis=1)
+    for b in range(batch):
+        ref = o.matvec(t, payload, xs[b].astype(np.float64), rows, cols)
+        assert_matvec_close(y[b], ref, xs[b], rowmax, f"{TYPES[t][0]} scale {scales[b]:g} b{b}/{batch}")
+
+
+@pytest.mark.parametrize("batch", [64, 100])
+@pytest.mark.parametrize("t", QUANT_TYPES, ids=lambda t: TYPES[t][0])
+def test_device_matvec_gemm_batches(torch_dev, t, batch):
+    """Prefill-sized batches (the MFMA dequant-GEMM for the block formats it
+    covers): ragged row and token tiles, every vector checked."""
+    announce("device_matvec_gemm", TYPES[t][0], 150, 1024, batch)
+    _device_matvec_check(torch_dev, t, 150, 1024, batch, seed=9500 + t)
+
+
+@pytest.mark.parametrize("t,rows,cols,batch", [(12, 4096, 4096, 96), (14, 4096, 4096, 64), (8, 1024, 14336, 72),
+                                               (12, 14336, 4096, 33)])
+def test_device_matvec_gemm_llama_shapes(torch_dev, t, rows, cols, batch):
+    """Llama-3-8B projection shapes at prefill batch sizes."""
+    announce("device_matvec_gemm_llama", TYPES[t][0], rows, cols, batch)
+    _device_matvec_check(torch_dev, t, rows, cols, batch, seed=9600 + rows + t)
+
+
+@pytest.mark.parametrize("t", [12, 14], ids=lambda t: TYPES[t][0])
+def test_device_matvec_random_payloads_gemm(torch_dev, t):
+    torch = torch_dev
+    from pyrite_amd import device
+
+    o = oracle()
+    rows, cols, batch = 70, 1024, 80
+    payload = _random_payload(t, rows, cols, 4400 + t)
+    announce("device_matvec_random_gemm", TYPES[t][0], rows, cols, batch)
+    xs = np.stack([o.normal(4500 + b, cols) for b in range(batch)]).astype(np.float32)
+    y = device.matvec(t, device.upload(payload.tobytes()), torch.from_numpy(xs).cuda(), rows, cols).cpu().numpy()
+    wd = o.dequantize_rows(t, payload, rows, cols).reshape(rows, cols)
+    rowmax = np.abs(wd).max(axis=1)
+    for b in range(batch):
+        ref = o.matvec(t, payload, xs[b].astype(np.float64), rows, cols)
+        assert_matvec_close(y[b], ref, xs[b], rowmax, f"{TYPES[t][0]} random b{b}/{batch}")
