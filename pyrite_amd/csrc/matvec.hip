@@ -18,8 +18,11 @@ int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch
         const char* v = getenv("PYRITE_MATVEC_PATH");  // "valu" forces the VALU kernels
         return (v && v[0] == 'v') ? 1 : 0;
     }();
+    // the MFMA kernels address a 32-row tile's weights with 32-bit offsets
+    const bool mfma = g.bs > 1 && !forced && mx_type_supported(type) &&
+                      32ull * (max_cols / g.bs * g.bpb) + 16 < 0x7FFFFFFFull;
     // prefill-sized batches: the MFMA dequant-GEMM, one launch per matrix
-    if (g.bs > 1 && !forced && batch >= kGemmMinBatch && mx_type_supported(type)) {
+    if (mfma && batch >= kGemmMinBatch) {
         for (size_t i = 0; i < n; ++i) {
             const int rc = mg_launch(type, mats[i], batch, al, stream, i == 0 ? start : nullptr,
                                      i + 1 == n ? stop : nullptr);
@@ -27,7 +30,7 @@ int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch
         }
         return 0;
     }
-    if (g.bs > 1 && !forced && batch >= 3 && mx_type_supported(type)) {
+    if (mfma && batch >= 3) {
         for (size_t done = 0; done < batch; done += 8) {
             const size_t c = batch - done < 8 ? batch - done : 8;
             const int rc = mx_group_launch(type, mats, n, c, done, al, stream, done == 0 ? start : nullptr,

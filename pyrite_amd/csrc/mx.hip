@@ -1,12 +1,17 @@
 // MFMA dequant-matvec for the GGML block formats (batch 1..8), gfx950.
 // Fragment construction and block formats: mx_traits.h.
 //
-// Schedule: a workgroup (4 waves) owns a 32-row tile (two 16-row MFMA column
-// tiles sharing the A fragment); its waves split the row's blocks round-robin
-// and the 4 partial results are summed in LDS in a fixed order, so results are
-// deterministic.  Workgroups loop over tiles.  The A fragments of the whole
-// row (or of a K chunk when they exceed the LDS budget) are built once per
-// workgroup in LDS, compacted to the token-parts in use (MB = 2 * tokens).
+// Schedule: a workgroup (4 waves) owns a task = a 32-row tile of one matrix
+// and a K part.  It first issues every load of the task at once: its
+// activations (unless already staged) and the tile's weight bytes of the part
+// as 16-byte buffer loads (coalesced, bounds-checked by the buffer range so
+// rows past the matrix read as zero), then parks the weights in LDS and
+// converts the activations into fp16 hi/lo A fragments in LDS.  Its waves
+// then split the part's blocks round-robin, decode B fragments from LDS and
+// run the MFMAs; the 4 partial results are summed in LDS in a fixed order,
+// so results are deterministic.  K parts are sized so that a part's
+// fragments and weights fit in LDS with two workgroups per CU; matrices with
+// more parts are combined by the last part to arrive (split K).
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
@@ -33,6 +38,8 @@ struct MxDesc {
     int kpart_steps;      // 32-column steps per K part (a multiple of the block's steps)
     int tiles;            // ceil(rows / 32)
     int task_begin;       // first task of this matrix; tasks = ksplit * tiles
+    int nch;              // 16-byte chunks loaded per row and part
+    int rs;               // LDS bytes per row of the staged weights
     int pad;
 };
 
@@ -40,58 +47,44 @@ constexpr int kMxMaxGroup = 16;
 struct MxGroup {
     int n;
     int total_tasks;
+    int frag_bytes;       // LDS bytes reserved for A fragments (largest part of the group)
+    int pad;
     MxDesc d[kMxMaxGroup];
 };
 
 constexpr int kRedBytes = 4 * 2 * 64 * 4 * 4;  // [wave][row tile][lane][4] floats
-constexpr int kPF = 2;                          // blocks per wave loaded ahead of their use
+// LDS bytes for one part's A fragments and staged weights: with the
+// reduction area and the static arrays two workgroups fit in a CU's 160 KiB
+constexpr int kMxPartBudget = 71680;
+// largest number of 16-byte weight loads per thread and part
+constexpr int kMxMaxWLoads = 10;
+constexpr unsigned kBufferWord3 = 0x00020000u;  // raw (untyped) buffer access on gfx9
+
+// LDS row stride for a part of nbp blocks: the 16-byte chunks covering the
+// row's bytes from a 16-byte boundary, an odd number of them so that the 16
+// rows a wave decodes together fall in different banks
+template <int T> constexpr int mx_nch(int nbp) { return (15 + nbp * Mx<T>::BPB + 15) / 16; }
+template <int T> constexpr int mx_rs(int nbp) { return 16 * (mx_nch<T>(nbp) | 1); }
+template <int T, int MB> constexpr bool mx_part_fits(int nbp) {
+    return nbp * Mx<T>::STEPS * MB * 64 + 32 * mx_rs<T>(nbp) <= kMxPartBudget &&
+           32 * mx_nch<T>(nbp) <= 256 * kMxMaxWLoads;
+}
+// largest part (in blocks) of this format at this fragment height
+template <int T, int MB> constexpr int mx_max_blocks() {
+    int nb = 1;
+    while (mx_part_fits<T, MB>(nb + 1)) ++nb;
+    return nb;
+}
+// activation items (8 values of one token) and weight loads per thread
+template <int T, int MB> constexpr int mx_xitems() {
+    return (mx_max_blocks<T, MB>() * Mx<T>::STEPS * 4 * (MB / 2) + 255) / 256;
+}
+template <int T, int MB> constexpr int mx_wloads() { return (32 * mx_nch<T>(mx_max_blocks<T, MB>()) + 255) / 256; }
 
 // Barrier for LDS hand-offs only: waits for this wave's LDS traffic, not for
 // its outstanding global loads (which may be blocks prefetched for later).
 __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// Largest finite |x| per token over steps [s0, s1) into tok_max (ordered
-// uint bits of a non-negative float; tok_max starts at zero).
-template <int MB>
-__device__ __forceinline__ void x_max(const MxDesc& d, int s0, int s1, int tid, unsigned* tok_max) {
-    constexpr int NT = MB / 2;
-    const int count = (s1 - s0) * 4 * NT;
-    for (int idx = tid; idx < count; idx += 256) {
-        const int s = s0 + idx / (4 * NT), rem = idx % (4 * NT);
-        const int gg = rem / NT, t = rem % NT;
-        if (t >= d.batch) continue;
-        const float* xp = d.X + t * d.ldx + 32 * s + 8 * gg;
-        const float4 a = ld_x4(xp), b = ld_x4(xp + 4);
-        const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        const float mx = finite_max8(xs);
-        if (mx > 0.f) atomicMax(&tok_max[t], __float_as_uint(mx));
-    }
-}
-
-// A fragments of steps [s0, s1) into LDS, laid out [step][group][MB] x 16 bytes
-// (8 halves: hi or lo parts of x[t][32 s + 8 group + i] * 2^-e_t, row 2t + p),
-// e_t the token's normalising exponent from tok_max.
-template <int MB>
-__device__ __forceinline__ void stage_x(const MxDesc& d, int s0, int s1, int tid, const unsigned* tok_max,
-                                        uint4* frag) {
-    constexpr int NT = MB / 2;
-    const int count = (s1 - s0) * 4 * NT;
-    for (int idx = tid; idx < count; idx += 256) {
-        const int s = idx / (4 * NT), rem = idx % (4 * NT);
-        const int gg = rem / NT, t = rem % NT;
-        uint4 hi = make_uint4(0u, 0u, 0u, 0u), lo = hi;
-        if (t < d.batch) {
-            const float* xp = d.X + t * d.ldx + 32 * (s0 + s) + 8 * gg;
-            const float4 a = ld_x4(xp), b = ld_x4(xp + 4);
-            const float xs[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            split8(xs, norm_exp(__uint_as_float(tok_max[t])), hi, lo);
-        }
-        uint4* f = frag + (s * 4 + gg) * MB + 2 * t;
-        f[0] = hi;
-        f[1] = lo;
-    }
 }
 
 // One block of two 16-row column tiles: B fragments, MFMAs, block epilogue.
@@ -125,17 +118,24 @@ __device__ __forceinline__ void mx_block(const typename Mx<T>::Raw& ra, const ty
 }
 
 template <int T, int MB, bool AL>
-__global__ __launch_bounds__(256) void mx_kernel(const MxGroup grp) {
+__global__ __launch_bounds__(256, 2) void mx_kernel(const MxGroup grp) {
     using F = Mx<T>;
+    constexpr int NT = MB / 2, XI = mx_xitems<T, MB>(), SPI = 256 / (4 * NT), WI = mx_wloads<T, MB>();
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     float* red = reinterpret_cast<float*>(smem);
     uint4* frag = reinterpret_cast<uint4*>(smem + kRedBytes);
-    __shared__ unsigned tok_max[8];
+    uint8_t* wlds = smem + kRedBytes + grp.frag_bytes;
+    // largest finite |x| per token, double-buffered over stagings (ordered
+    // uint bits of a non-negative float)
+    __shared__ unsigned tok_max[2][8];
     __shared__ int last_flag;
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
-    int staged_mi = -1, staged_kp = -1;
+    // staging role: token xt, 8-column group xg of steps xs + SPI * k
+    const int xt = tid % NT, xg = (tid / NT) % 4, xs = tid / (4 * NT);
+    int staged_mi = -1, staged_kp = -1, tb = 1;
+    if (tid < 8) tok_max[0][tid] = 0u;
 
     for (int task = blockIdx.x; task < grp.total_tasks; task += gridDim.x) {
         int mi = 0;
@@ -150,58 +150,101 @@ __global__ __launch_bounds__(256) void mx_kernel(const MxGroup grp) {
         const int s1 = (s0 + kps < (d.cols >> 5)) ? s0 + kps : (d.cols >> 5);
         const int kb0 = s0 / F::STEPS;
         const int kb1 = (s1 / F::STEPS < nblk) ? s1 / F::STEPS : nblk;
+        const int nch = d.nch, rs = d.rs;
 
-        const long long r0 = (long long)tile * 32 + n, r1 = r0 + 16;
-        const uint8_t* rp0 = d.W + (r0 < rows ? r0 : rows - 1) * d.row_bytes;
-        const uint8_t* rp1 = d.W + (r1 < rows ? r1 : rows - 1) * d.row_bytes;
-
-        // first blocks of this wave, loaded before the (possible) staging.
-        // Loads are unconditional (block index clamped to the part's last
-        // block) so every path has the same loads in flight and the waits
-        // before a decode cover only the older loads.
-        typename F::Raw ra[kPF], rb[kPF];
-        int blk = kb0 + w;
-        auto load_blk = [&](int bq, typename F::Raw& a0, typename F::Raw& a1) {
-            const int bc = bq < kb1 ? bq : kb1 - 1;
-            F::template load<AL>(rp0 + (size_t)bc * F::BPB, g, a0);
-            F::template load<AL>(rp1 + (size_t)bc * F::BPB, g, a1);
-        };
-        // short parts (one block per wave at most) skip the prefetch pipeline
-        const bool piped = kb1 - kb0 > 4;
-        load_blk(blk, ra[0], rb[0]);
-        if (piped) {
+        // 1. activations of the part, unless this workgroup staged them last
+        const bool stage = mi != staged_mi || kp != staged_kp;
+        float xv[XI][8];
+        if (stage) {
+            const bool tok_ok = xt < d.batch;
+            const float* xp = d.X + (unsigned long long)(tok_ok ? xt : 0) * d.ldx + 8 * xg;
 #pragma unroll
-            for (int p = 1; p < kPF; ++p) load_blk(blk + 4 * p, ra[p], rb[p]);
+            for (int k = 0; k < XI; ++k) {
+                const int s = s0 + xs + SPI * k;
+                if (tok_ok && s < s1) {
+                    const float4 u = ld_x4(xp + 32 * s), v = ld_x4(xp + 32 * s + 4);
+                    xv[k][0] = u.x; xv[k][1] = u.y; xv[k][2] = u.z; xv[k][3] = u.w;
+                    xv[k][4] = v.x; xv[k][5] = v.y; xv[k][6] = v.z; xv[k][7] = v.w;
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) xv[k][i] = 0.f;
+                }
+            }
         }
 
-        if (mi != staged_mi || kp != staged_kp) {
+        // 2. the tile's weight bytes of the part: row r's chunk c is the 16
+        // bytes at (its part start rounded down to 16) + 16 c.  The buffer
+        // covers the tile's rows from and to a 16-byte boundary (never past
+        // the page holding the matrix's last byte), so every chunk lies wholly
+        // inside or wholly outside it, and outside reads as zero.
+        const long long trow0 = (long long)tile * 32;
+        const int trows = rows - trow0 < 32 ? (int)(rows - trow0) : 32;
+        const uint8_t* tw = d.W + trow0 * d.row_bytes;
+        const uint8_t* tbase = reinterpret_cast<const uint8_t*>(reinterpret_cast<uintptr_t>(tw) & ~(uintptr_t)15);
+        const unsigned pre = (unsigned)(tw - tbase);
+        const unsigned part0 = pre + (unsigned)kb0 * F::BPB;  // row 0's part start in the buffer
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint8_t*>(tbase), (short)0, (int)((pre + (unsigned)trows * (unsigned)d.row_bytes + 15u) & ~15u),
+            (int)kBufferWord3);
+        uint4 wv[WI];
+#pragma unroll
+        for (int k = 0; k < WI; ++k) {
+            const int c = tid + 256 * k;
+            const int r = c / nch, col = c - r * nch;
+            // chunks past the 32 rows get an offset beyond the buffer: zero, no traffic
+            const unsigned off = r < 32 ? ((part0 + (unsigned)r * (unsigned)d.row_bytes) & ~15u) + 16u * col
+                                        : 0xFFFFFFF0u;
+            typedef unsigned u4v __attribute__((ext_vector_type(4)));
+            const u4v v = __builtin_amdgcn_raw_buffer_load_b128(rsrc, (int)off, 0, 0);
+            wv[k] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+
+        // 3. park the weights and build the A fragments
+        lds_barrier();  // the previous task's fragments, weights and partials are consumed
+#pragma unroll
+        for (int k = 0; k < WI; ++k) {
+            const int c = tid + 256 * k;
+            const int r = c / nch, col = c - r * nch;
+            if (r < 32) *reinterpret_cast<uint4*>(wlds + r * rs + 16 * col) = wv[k];
+        }
+        if (stage) {
             // Each token is staged scaled by the power of two 2^-e that brings
             // its largest finite |x| into [2^14, 2^15) (see norm_exp); results
-            // are multiplied back by 2^e (exact).
+            // are multiplied back by 2^e (exact).  A thread's items all belong
+            // to token xt.
+            float mx = 0.f;
+#pragma unroll
+            for (int k = 0; k < XI; ++k) mx = fmaxf(mx, finite_max8(xv[k]));
+            tb ^= 1;
+            if (tid < 8) tok_max[tb ^ 1][tid] = 0u;
+            if (mx > 0.f) atomicMax(&tok_max[tb][xt], __float_as_uint(mx));
             lds_barrier();
-            if (tid < 8) tok_max[tid] = 0u;
-            lds_barrier();
-            x_max<MB>(d, s0, s1, tid, tok_max);
-            lds_barrier();
-            stage_x<MB>(d, s0, s1, tid, tok_max, frag);
-            lds_barrier();
+            const int e = norm_exp(__uint_as_float(tok_max[tb][xt]));
+#pragma unroll
+            for (int k = 0; k < XI; ++k) {
+                const int s = xs + SPI * k;
+                if (s0 + s < s1) {
+                    uint4 hi, lo;
+                    split8(xv[k], e, hi, lo);
+                    uint4* f = frag + (s * 4 + xg) * MB + 2 * xt;
+                    f[0] = hi;
+                    f[1] = lo;
+                }
+            }
             staged_mi = mi;
             staged_kp = kp;
         }
+        lds_barrier();
 
+        // 4. this wave's blocks: rows n and n + 16 of the tile
+        const uint8_t* p0 = wlds + n * rs + ((part0 + (unsigned)n * (unsigned)d.row_bytes) & 15u);
+        const uint8_t* p1 = wlds + (n + 16) * rs + ((part0 + (unsigned)(n + 16) * (unsigned)d.row_bytes) & 15u);
         f4v acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        // each slot is refilled right after its block is decoded, so the other
-        // slots' loads stay in flight during every decode
-        if (!piped) {
-            if (blk < kb1) mx_block<T, MB>(ra[0], rb[0], frag + (blk * F::STEPS - s0) * 4 * MB, g, n, acc);
-        } else while (blk < kb1) {
-#pragma unroll
-            for (int p = 0; p < kPF; ++p) {
-                const int bq = blk + 4 * p;
-                if (bq < kb1) mx_block<T, MB>(ra[p], rb[p], frag + (bq * F::STEPS - s0) * 4 * MB, g, n, acc);
-                load_blk(bq + 4 * kPF, ra[p], rb[p]);
-            }
-            blk += 4 * kPF;
+        for (int b = kb0 + w; b < kb1; b += 4) {
+            typename F::Raw ra, rb;
+            F::template load<AL>(p0 + (b - kb0) * F::BPB, g, ra);
+            F::template load<AL>(p1 + (b - kb0) * F::BPB, g, rb);
+            mx_block<T, MB>(ra, rb, frag + (b * F::STEPS - s0) * 4 * MB, g, n, acc);
         }
 
         // Sum the 4 waves' partials in a fixed order.  Lane (n, g) of wave w
@@ -220,7 +263,7 @@ __global__ __launch_bounds__(256) void mx_kernel(const MxGroup grp) {
                 const float* q = red + ((ww * 2 + rt) * 64 + src) * 4;
                 sum += q[j] + q[j + 1];
             }
-            sum = __builtin_amdgcn_ldexpf(sum, norm_exp(__uint_as_float(tok_max[t])));
+            sum = __builtin_amdgcn_ldexpf(sum, norm_exp(__uint_as_float(tok_max[tb][t])));
         }
         const int trow = rt * 16 + nn;
         const long long row = (long long)tile * 32 + trow;
@@ -250,41 +293,40 @@ __global__ __launch_bounds__(256) void mx_kernel(const MxGroup grp) {
 // ---------------------------------------------------------------- launcher
 
 constexpr long long kMxTargetWgs = 1024;
-// bytes of A fragments per workgroup: with the reduction area and the small
-// static arrays the workgroup stays within 64 KiB of LDS
-constexpr int kMxLdsBudget = 65536 - kRedBytes - 512;
 
 struct MxPlanOut {
     long long tasks;
     size_t part_floats;
     size_t counters;
     int max_kps;
+    int max_wbytes;
 };
 
 template <int T, int MB>
 static MxPlanOut mx_plan(MxGroup& grp) {
     using F = Mx<T>;
-    MxPlanOut out{0, 0, 0, 0};
-    int kc = kMxLdsBudget / (MB * 64);
-    kc -= kc % F::STEPS;
+    MxPlanOut out{0, 0, 0, 0, 0};
+    constexpr int kmax = mx_max_blocks<T, MB>();
     for (int i = 0; i < grp.n; ++i) {
         MxDesc& d = grp.d[i];
-        const int nsteps = d.cols / 32, nblk = d.cols / F::BS;
+        const int nblk = d.cols / F::BS;
         d.tiles = (d.rows + 31) / 32;
-        // K parts: only as many as the LDS budget for the activations needs
-        // (a matrix's parts depend on its own shape, never on its group)
-        int ks = (nsteps + kc - 1) / kc;
-        int bpp = (nblk + ks - 1) / ks;  // blocks per part
-        ks = (nblk + bpp - 1) / bpp;
-        d.ksplit = ks;
+        // K parts: only as many as the LDS budget needs, balanced (a
+        // matrix's parts depend on its own shape, never on its group)
+        const int ks = (nblk + kmax - 1) / kmax;
+        const int bpp = (nblk + ks - 1) / ks;  // blocks per part
+        d.ksplit = (nblk + bpp - 1) / bpp;
         d.kpart_steps = bpp * F::STEPS;
+        d.nch = mx_nch<T>(bpp);
+        d.rs = mx_rs<T>(bpp);
         d.task_begin = (int)out.tasks;
-        out.tasks += (long long)ks * d.tiles;
-        if (ks > 1) {
-            out.part_floats += (size_t)ks * d.tiles * 256;
+        out.tasks += (long long)d.ksplit * d.tiles;
+        if (d.ksplit > 1) {
+            out.part_floats += (size_t)d.ksplit * d.tiles * 256;
             out.counters += d.tiles;
         }
         if (d.kpart_steps > out.max_kps) out.max_kps = d.kpart_steps;
+        if (32 * d.rs > out.max_wbytes) out.max_wbytes = 32 * d.rs;
     }
     return out;
 }
@@ -358,7 +400,13 @@ static hipError_t mx_launch_group(MxGroup& grp, hipStream_t stream, hipEvent_t s
         }
     }
     const long long wgs = plan.tasks < kMxTargetWgs ? plan.tasks : kMxTargetWgs;
-    const size_t lds = kRedBytes + (size_t)plan.max_kps * 4 * MB * 16;
+    grp.frag_bytes = plan.max_kps * 4 * MB * 16;
+    const size_t lds = kRedBytes + (size_t)grp.frag_bytes + (size_t)plan.max_wbytes;
+    // more than 64 KiB of dynamic LDS: declare the kernel's largest need once
+    static const hipError_t lds_ok = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&mx_kernel<T, MB, AL>), hipFuncAttributeMaxDynamicSharedMemorySize,
+        kRedBytes + kMxPartBudget);
+    if (lds_ok != hipSuccess) return lds_ok;
     if (start || stop)
         hipExtLaunchKernelGGL((mx_kernel<T, MB, AL>), dim3((unsigned)wgs), dim3(256), (uint32_t)lds, stream, start,
                               stop, 0, grp);
