@@ -14,10 +14,7 @@ int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch
     bool al = false;
     size_t max_cols = 0;
     if (const int rc = validate_group(g, mats, n, batch, &al, &max_cols)) return rc;
-    static const int forced = [] {
-        const char* v = getenv("PYRITE_MATVEC_PATH");  // "valu" forces the VALU kernels
-        return (v && v[0] == 'v') ? 1 : 0;
-    }();
+    const bool forced = matvec_path_env() == 'v';
     // the MFMA kernels address a 32-row tile's weights with 32-bit offsets
     const bool mfma = g.bs > 1 && !forced && mx_type_supported(type) &&
                       32ull * (max_cols / g.bs * g.bpb) + 16 < 0x7FFFFFFFull;

@@ -48,40 +48,55 @@ struct MvDesc {
 };
 
 // How a workgroup fetches 16 activations (vector b, columns 16j..16j+15)
-// when it stages them.  XDirect: row b of X.  XGather: row xrow[b] of X, or
-// zeros.  XSwiglu: silu(X[b]) * X2[b] (pyrite/tensor_ops.py:509-510: v / (1 +
+// when it stages them: fetch() issues the loads into F, finish() turns F into
+// the 16 values.  XDirect: row b of X.  XGather: row xrow[b] of X, or zeros.
+// XSwiglu: silu(X[b]) * X2[b] (pyrite/tensor_ops.py:509-510: v / (1 +
 // exp(-v)) for v > -60, else 0), in fp64, rounded to fp32.
 struct XDirect {
-    __device__ __forceinline__ static void load16(const MvDesc& d, int b, int j, float4 (&v)[4]) {
+    struct F { float4 v[4]; };
+    __device__ __forceinline__ static void fetch(const MvDesc& d, int b, int j, F& f) {
         const float* p = d.X + b * d.ldx + 16 * j;
-        v[0] = ld_x4(p); v[1] = ld_x4(p + 4); v[2] = ld_x4(p + 8); v[3] = ld_x4(p + 12);
+        f.v[0] = ld_x4(p); f.v[1] = ld_x4(p + 4); f.v[2] = ld_x4(p + 8); f.v[3] = ld_x4(p + 12);
+    }
+    __device__ __forceinline__ static void finish(const F& f, float4 (&v)[4]) {
+        v[0] = f.v[0]; v[1] = f.v[1]; v[2] = f.v[2]; v[3] = f.v[3];
     }
 };
 struct XGather {
-    __device__ __forceinline__ static void load16(const MvDesc& d, int b, int j, float4 (&v)[4]) {
+    struct F { float4 v[4]; bool missing; };
+    __device__ __forceinline__ static void fetch(const MvDesc& d, int b, int j, F& f) {
         const int t = d.xrow[b];
-        if (t < 0) {
-            v[0] = v[1] = v[2] = v[3] = make_float4(0.f, 0.f, 0.f, 0.f);
-            return;
-        }
-        const float* p = d.X + (unsigned long long)t * d.ldx + 16 * j;
-        v[0] = ld_x4(p); v[1] = ld_x4(p + 4); v[2] = ld_x4(p + 8); v[3] = ld_x4(p + 12);
+        f.missing = t < 0;  // a missing row reads row 0 (always present) and becomes zeros
+        const float* p = d.X + (unsigned long long)(f.missing ? 0 : t) * d.ldx + 16 * j;
+        f.v[0] = ld_x4(p); f.v[1] = ld_x4(p + 4); f.v[2] = ld_x4(p + 8); f.v[3] = ld_x4(p + 12);
+    }
+    __device__ __forceinline__ static void finish(const F& f, float4 (&v)[4]) {
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = f.missing ? z : f.v[k];
     }
 };
 struct XSwiglu {
-    __device__ __forceinline__ static float f(float g, float u) {
+    struct F { float4 g[4], u[4]; };
+    __device__ __forceinline__ static float act(float g, float u) {
         const double gd = g;
         const double s = gd > -60.0 ? gd / (1.0 + exp(-gd)) : 0.0;
         return (float)(s * (double)u);
     }
-    __device__ __forceinline__ static void load16(const MvDesc& d, int b, int j, float4 (&v)[4]) {
+    __device__ __forceinline__ static void fetch(const MvDesc& d, int b, int j, F& f) {
         const float* pg = d.X + b * d.ldx + 16 * j;
         const float* pu = d.X2 + b * d.ldx + 16 * j;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const float4 g = ld_x4(pg + 4 * k), u = ld_x4(pu + 4 * k);
-            v[k] = make_float4(f(g.x, u.x), f(g.y, u.y), f(g.z, u.z), f(g.w, u.w));
+            f.g[k] = ld_x4(pg + 4 * k);
+            f.u[k] = ld_x4(pu + 4 * k);
         }
+    }
+    __device__ __forceinline__ static void finish(const F& f, float4 (&v)[4]) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            v[k] = make_float4(act(f.g[k].x, f.u[k].x), act(f.g[k].y, f.u[k].y), act(f.g[k].z, f.u[k].z),
+                               act(f.g[k].w, f.u[k].w));
     }
 };
 
@@ -181,20 +196,32 @@ __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* sm
 #pragma unroll
             for (int r = 0; r < R; ++r) Un::template load<AL>(rp[r] + (size_t)blk * BPB, (int)part, dst[r]);
         };
-        Raw ra[R], rb[R];
-        load_item(ra, rp_cur, li);  // first weights in flight while the activations are staged
-
         // Per-16-column sums of X (and of |X| for BD; with XL, the padded copy
-        // of X) in LDS, one pass.
+        // of X) in LDS, one pass.  The thread's first 16 activations are
+        // loaded before the first weights, so waiting for them does not wait
+        // for the weights (loads complete in order).
         lds_f* xs16 = (lds_f*)(smem);  // address-space cast: smem is LDS
         const int ldxl = cols + (cols / PADI) * 4;
         const int n16r = (B * n16 + 3) & ~3;
         lds_f* xa16 = xs16 + n16r;
         lds_f* xl = xs16 + (BD ? 2 * n16r : n16r);
+        const int i0 = (int)threadIdx.x < B * n16 ? (int)threadIdx.x : 0;
+        typename XS::F xf0;
+        XS::fetch(d, i0 / n16, i0 - (i0 / n16) * n16, xf0);
+
+        Raw ra[R], rb[R];
+        load_item(ra, rp_cur, li);  // first weights in flight while the activations are staged
+
         for (int i = threadIdx.x; i < B * n16; i += blockDim.x) {
             const int b = i / n16, j = i - b * n16;
             float4 v4[4];
-            XS::load16(d, b, j, v4);
+            if (i == (int)threadIdx.x) {
+                XS::finish(xf0, v4);
+            } else {
+                typename XS::F xf;
+                XS::fetch(d, b, j, xf);
+                XS::finish(xf, v4);
+            }
             const float4 a = v4[0], c = v4[1], e = v4[2], f = v4[3];
             xs16[i] = (((a.x + a.y) + (a.z + a.w)) + ((c.x + c.y) + (c.z + c.w))) +
                       (((e.x + e.y) + (e.z + e.w)) + ((f.x + f.y) + (f.z + f.w)));
@@ -480,6 +507,15 @@ static hipError_t launch_type(int batch, const MvGroup& g, hipStream_t s, Launch
     case 8: return launch_group<T, 8, AL, BD>(g, s, ev);
     default: return hipErrorInvalidValue;
     }
+}
+
+// PYRITE_MATVEC_PATH=valu keeps matvecs on the VALU kernels (no MFMA).
+static char matvec_path_env() {
+    static const char c = [] {
+        const char* v = getenv("PYRITE_MATVEC_PATH");
+        return v ? v[0] : '\0';
+    }();
+    return c;
 }
 
 // Largest instantiated batch chunk (8, 4, 2, 1) not above `left` whose LDS

@@ -332,3 +332,35 @@ def test_device_matvec_random_payloads_gemm(torch_dev, t):
     for b in range(batch):
         ref = o.matvec(t, payload, xs[b].astype(np.float64), rows, cols)
         assert_matvec_close(y[b], ref, xs[b], rowmax, f"{TYPES[t][0]} random b{b}/{batch}")
+
+
+@pytest.mark.parametrize("batch", [1, 2, 5])
+@pytest.mark.parametrize("t", [12, 14, 2, 8, 23, 0], ids=lambda t: TYPES[t][0])
+def test_device_matvec_nonfinite_activations(torch_dev, t, batch):
+    """An infinite or NaN activation in one vector: the rows it reaches are
+    non-finite, as in the reference (which of inf and NaN may differ: the
+    kernels factor the block scales out of the sums, so 0 * inf can appear
+    where the reference multiplies a dequantized weight), and every finite
+    reference row is within the bar."""
+    torch = torch_dev
+    from pyrite_amd import device
+
+    o = oracle()
+    rows, cols = 40, 512
+    payload = _weights(t, rows, cols, 4950 + t)
+    xs = np.stack([o.normal(4960 + b, cols) for b in range(batch)]).astype(np.float32)
+    xs[0, 7] = np.float32(np.inf)
+    if batch > 1:
+        xs[1, 100] = np.float32(np.nan)
+    announce("device_matvec_nonfinite", TYPES[t][0], rows, cols, batch)
+    y = device.matvec(t, device.upload(payload.tobytes()), torch.from_numpy(xs).cuda(), rows, cols).cpu().numpy()
+    wd = o.dequantize_rows(t, payload, rows, cols).reshape(rows, cols)
+    rowmax = np.abs(wd).max(axis=1)
+    for b in range(batch):
+        ref = o.matvec(t, payload, xs[b].astype(np.float64), rows, cols)
+        assert np.array_equal(np.isfinite(y[b]), np.isfinite(ref)), f"b{b}: finite rows differ"
+        fin = np.isfinite(ref)
+        if fin.any():
+            err = np.abs(y[b][fin].astype(np.float64) - ref[fin])
+            xf = np.where(np.isfinite(xs[b]), xs[b], 0.0)
+            assert np.all(err <= 1e-4 * np.linalg.norm(xf) * rowmax[fin]), f"b{b}: finite rows off"
