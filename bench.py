@@ -156,6 +156,38 @@ def quantized_normal(np, quantize, t, n, seed):
     return quantize(t, w)
 
 
+COPY_BYTES = 256 << 20
+
+
+def copy_calibration(torch, stream):
+    """Plain device copies of 256 MiB (read 256 MiB, write 256 MiB per copy):
+    the known-size reference for scaling the FETCH_SIZE / WRITE_SIZE counters."""
+    src = torch.randn(COPY_BYTES // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"workload": "torch copy_ of 256 MiB fp32, 5 times", "read_bytes_per_copy": COPY_BYTES,
+            "write_bytes_per_copy": COPY_BYTES}
+
+
+def launch_kernel_name(batch: int) -> str:
+    """Kernel that pyrite_dev_matvec_grouped runs for this type and batch (block formats)."""
+    return "mx_kernel (MFMA)" if batch >= 3 else "mv_kernel (VALU)"
+
+
+def load_traffic(key: str):
+    """HBM bytes per launch of a sweep launch ("<type>_b<batch>") from the committed
+    FETCH_SIZE / WRITE_SIZE profile (profiles/traffic_sweep.json), or None."""
+    path = ROOT / "profiles" / "traffic_sweep.json"
+    try:
+        data = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = data.get("launches", {}).get(key)
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
 def bench_config1(torch, np, quantize, stream, device):
     """Single Q4_K 3072x1024 matvec (Qwen3-0.6B ffn_up), batch 1."""
     rows, cols = 3072, 1024
@@ -289,7 +321,8 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="skip the LM-head, MoE and Llama configurations")
     ap.add_argument("--only", default=None,
                     help="run only the named extra configuration (config1_q4k_3072x1024, config3_lm_head, "
-                         "config4_moe, config5_llama3_8b_layer) and print its JSON; for profiling")
+                         "config4_moe, config5_llama3_8b_layer, copy_calibration) and print its JSON; "
+                         "for profiling")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures the dequant-matvec path on one GPU; runs on more than one GPU "
@@ -313,7 +346,8 @@ def main() -> int:
         fns = {"config1_q4k_3072x1024": lambda: bench_config1(torch, np, quantize, stream, device),
                "config3_lm_head": lambda: bench_lm_head(torch, np, quantize, stream, device),
                "config4_moe": lambda: bench_moe(torch, np, quantize, stream, device),
-               "config5_llama3_8b_layer": lambda: bench_llama(torch, np, quantize, stream, device, lib, sptr)}
+               "config5_llama3_8b_layer": lambda: bench_llama(torch, np, quantize, stream, device, lib, sptr),
+               "copy_calibration": lambda: copy_calibration(torch, stream)}
         print(json.dumps({args.only: fns[args.only]()}), flush=True)
         return 0
     log("quantizing and uploading the sweep weights")
@@ -414,9 +448,10 @@ def main() -> int:
                                       "gbs": nbytes / avg / 1e9}
     dominant = max(per_kernel, key=lambda k: per_kernel[k]["total_s"])
     dk = per_kernel[dominant]
+    dom_batch = int(dominant.rsplit("_b", 1)[1])
     roofline = {"bound": "hbm", "achieved": round(dk["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": f"mv_kernel {dominant} (grouped launch over the 7 projections)",
+                "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(dominant),
+                "kernel": f"{launch_kernel_name(dom_batch)} {dominant} (grouped launch over the 7 projections)",
                 "avg_launch_us": round(dk["avg_us"], 3), "bytes_per_launch": dk["bytes_per_launch"],
                 "timing": timing_source}
 
