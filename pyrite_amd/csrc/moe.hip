@@ -28,6 +28,7 @@
 //   moe_combine_kernel  out = sum of w * down-out in slot order (fp64 inside)
 #include "dequant.h"
 #include "mv_kernel.h"
+#include "mx_traits.h"
 
 namespace pyrite {
 
@@ -570,6 +571,348 @@ static bool moe_fused_ok(int type, int MB, size_t cols) {
     return bytes <= 65536;
 }
 
+// ---------------------------------------------------------------- MFMA experts
+// Batches of 32 tokens and more: chunks of kMoeMxTok tokens per expert, and
+// per chunk the expert's rows multiplied on the matrix cores
+// (v_mfma_f32_16x16x32_f16 with the exact fp16 fragments of mx_traits.h; A
+// row 2t + p = fp16 hi (p = 0) / lo (p = 1) part of token t, each token
+// scaled by the power of two 2^-e_t that brings its largest finite |x| into
+// [2^14, 2^15), the results multiplied back by 2^e_t).
+//   moe_xfrag_kernel  one workgroup per chunk: gathers the chunk's tokens and
+//                     writes their A fragments and exponents once
+//   moe_gu_kernel     items (chunk, row part): gate and up rows of the part
+//                     against the chunk's fragments (copied to LDS), writes
+//                     silu(gate) * up and the pair's largest finite |act|
+//   moe_dn_kernel     items (chunk, row part): down rows against the chunk's
+//                     activations (staged as fragments from act)
+// A workgroup takes a contiguous range of items (consecutive items share a
+// chunk); its 4 waves walk the part in 128-row tiles (two 16-row MFMA tiles
+// per wave) with kMoeMxPF blocks of weights in flight per wave.
+constexpr int kMoeMxTok = 8;
+constexpr int kMoeMxRows = 128;
+constexpr int kMoeMxMaxCols = 3072;  // activation fragments of a chunk: cols * 32 bytes of LDS
+constexpr int kMoeMxPF = 3;          // blocks per wave in flight
+constexpr int kMoeMxMaxPart = 512;   // rows per part at most (results buffered in LDS)
+
+struct MoeMxArgs {
+    const uint8_t* W[2];        // stacked [E][rows][row_bytes] (gate, up) or (down)
+    unsigned long long slice;   // bytes per expert
+    unsigned long long row_bytes;
+    int rows, cols;
+    int parts, part_rows;       // row parts per chunk; rows per part (a multiple of kMoeMxRows)
+    const uint4* xf;            // [chunk][cols / 32][4][16] fragments (moe_gu_kernel)
+    const int* xe;              // [chunk][kMoeMxTok] exponents (moe_gu_kernel)
+    const float* act;           // [pairs][cols] silu(gate) * up (moe_dn_kernel)
+    unsigned* amax;             // [pairs] largest finite |act| (ordered uint bits)
+    float* Y;                   // moe_gu_kernel: act [pairs][rows]; moe_dn_kernel: [pairs][rows]
+    const int* coff;
+    const int* poff;
+    const int* totals;
+    int E;
+};
+
+// silu(g) * u (pyrite/tensor_ops.py:509-510: v / (1 + exp(-v)) for v > -60, else 0) in fp32
+__device__ __forceinline__ float moe_act(float g, float u) {
+    return g > -60.f ? g / (1.f + expf(-g)) * u : 0.f;
+}
+
+__device__ __forceinline__ int moe_expert_of(const int* coff, int E, int chunk) {
+    int lo = 0, hi = E;  // expert e with coff[e] <= chunk < coff[e + 1]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (coff[mid] <= chunk) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+// One workgroup per chunk: the gathered tokens' fragments, exponents, and the
+// chunk's act maxima cleared for moe_gu_kernel.
+__global__ __launch_bounds__(256) void moe_xfrag_kernel(const float* X, unsigned long long ldx, int cols,
+                                                        const int* pair_tok, const int* coff, const int* poff,
+                                                        const int* totals, int E, uint4* xf, int* xe,
+                                                        unsigned* amax) {
+    __shared__ unsigned tok_max[kMoeMxTok];
+    const int chunk = blockIdx.x;
+    if (chunk >= totals[1]) return;
+    const int e = moe_expert_of(coff, E, chunk);
+    const int pair0 = poff[e] + (chunk - coff[e]) * kMoeMxTok;
+    const int tid = threadIdx.x;
+    if (tid < kMoeMxTok) {
+        tok_max[tid] = 0u;
+        amax[pair0 + tid] = 0u;
+    }
+    __syncthreads();
+    const int steps = cols >> 5, count = steps * 4 * kMoeMxTok;
+    auto load8 = [&](int idx, int& t, int& gg, int& st, float (&v)[8]) {
+        t = idx % kMoeMxTok;
+        gg = (idx / kMoeMxTok) & 3;
+        st = idx / (4 * kMoeMxTok);
+        const int tok = pair_tok[pair0 + t];
+        if (tok < 0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.f;
+            return;
+        }
+        const float* p = X + (unsigned long long)tok * ldx + 32 * st + 8 * gg;
+        const float4 x0 = ld_x4(p), x1 = ld_x4(p + 4);
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+    };
+    for (int idx = tid; idx < count; idx += 256) {
+        int t, gg, st;
+        float v[8];
+        load8(idx, t, gg, st, v);
+        const float mx = finite_max8(v);
+        if (mx > 0.f) atomicMax(&tok_max[t], __float_as_uint(mx));
+    }
+    __syncthreads();
+    uint4* out = xf + (size_t)chunk * steps * 64;
+    for (int idx = tid; idx < count; idx += 256) {
+        int t, gg, st;
+        float v[8];
+        load8(idx, t, gg, st, v);
+        uint4 h, l;
+        split8(v, norm_exp(__uint_as_float(tok_max[t])), h, l);
+        out[(st * 4 + gg) * 16 + 2 * t] = h;
+        out[(st * 4 + gg) * 16 + 2 * t + 1] = l;
+    }
+    if (tid < kMoeMxTok) xe[chunk * kMoeMxTok + tid] = norm_exp(__uint_as_float(tok_max[tid]));
+}
+
+// The block sequence of one wave over a row part of one or two matrices that
+// share the staged fragments: q runs over (tile, matrix, block); raw[p] holds
+// block q0 + p.  acc[j] collects matrix j of the current tile; done(tile)
+// is called after the last block of each tile.
+template <int T, bool AL, int NM, class Done>
+__device__ __forceinline__ void moe_mx_walk(const MoeMxArgs& a, int e, int row_lo, int row_hi, const uint4* frag,
+                                            f4v (&acc)[NM][2], Done done) {
+    using F = Mx<T>;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
+    const int nblk = a.cols / F::BS;
+    const int ntile = (row_hi - row_lo + kMoeMxRows - 1) / kMoeMxRows;
+    const int per_tile = NM * nblk;
+    const int nq = ntile * per_tile;
+    auto load_q = [&](int q, typename F::Raw& r0, typename F::Raw& r1) {
+        const int qq = q < nq ? q : nq - 1;
+        const int tile = qq / per_tile, rem = qq - tile * per_tile;
+        const int j = rem / nblk, b = rem - j * nblk;
+        const uint8_t* Wm = a.W[j] + (unsigned long long)e * a.slice;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            long long r = (long long)row_lo + (long long)tile * kMoeMxRows + 32 * w + 16 * h + n;
+            if (r >= a.rows) r = a.rows - 1;
+            F::template load<AL>(Wm + (unsigned long long)r * a.row_bytes + (size_t)b * F::BPB, g, h ? r1 : r0);
+        }
+    };
+    typename F::Raw ra[kMoeMxPF], rb[kMoeMxPF];
+#pragma unroll
+    for (int p = 0; p < kMoeMxPF; ++p) {
+        load_q(p, ra[p], rb[p]);
+        asm volatile("" ::: "memory");
+    }
+    for (int q0 = 0; q0 < nq; q0 += kMoeMxPF) {
+#pragma unroll
+        for (int p = 0; p < kMoeMxPF; ++p) {
+            const int q = q0 + p;
+            if (q < nq) {
+                const int tile = q / per_tile, rem = q - tile * per_tile;
+                const int j = rem / nblk, b = rem - j * nblk;
+                f4v D[2][F::NACC];
+#pragma unroll
+                for (int c = 0; c < F::NACC; ++c) D[0][c] = D[1][c] = f4v{0.f, 0.f, 0.f, 0.f};
+                const uint4* fb = frag + (size_t)b * F::STEPS * 4 * 16;
+#pragma unroll
+                for (int st = 0; st < F::STEPS; ++st) {
+                    const uint4 av = fb[(st * 4 + g) * 16 + n];
+                    const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
+                    const h8v A = __builtin_bit_cast(h8v, aw);
+                    uint32_t ba[F::NACC][4], bb[F::NACC][4];
+                    F::frag(ra[p], st, g, ba);
+                    F::frag(rb[p], st, g, bb);
+#pragma unroll
+                    for (int c = 0; c < F::NACC; ++c) {
+                        D[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8v, ba[c]), D[0][c], 0, 0, 0);
+                        D[1][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8v, bb[c]), D[1][c], 0, 0, 0);
+                    }
+                }
+                // j is wave-uniform: select the accumulator pair without dynamic indexing
+#pragma unroll
+                for (int jj = 0; jj < NM; ++jj) {
+                    if (jj == j) {
+                        F::epi(ra[p], D[0], acc[jj][0]);
+                        F::epi(rb[p], D[1], acc[jj][1]);
+                    }
+                }
+                if (rem == per_tile - 1) done(tile);
+            }
+            load_q(q + kMoeMxPF, ra[p], rb[p]);
+            // keep the refills in slot order: loads complete in order, so a
+            // slot refilled after a later one would make its wait cover both
+            asm volatile("" ::: "memory");
+        }
+    }
+}
+
+// Contiguous item range of this workgroup over `total` items.
+__device__ __forceinline__ void moe_item_range(long long total, long long& it0, long long& it1) {
+    const long long per = (total + gridDim.x - 1) / gridDim.x;
+    it0 = (long long)blockIdx.x * per;
+    it1 = it0 + per < total ? it0 + per : total;
+}
+
+// Results of a part wait in LDS ([tile row][token], after the fragments)
+// and are stored after the walk: global stores inside the walk would share
+// the load counter and cut the weight pipeline short.
+template <int T, bool AL>
+__global__ __launch_bounds__(256, 2) void moe_gu_kernel(const MoeMxArgs a) {
+    extern __shared__ float smem[];
+    uint4* frag = reinterpret_cast<uint4*>(smem);
+    float* res = smem + (size_t)a.cols * 8;  // [part_rows][kMoeMxTok]
+    __shared__ int tok_e[kMoeMxTok];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, n = lane & 15;
+    const int steps = a.cols >> 5;
+    long long it0, it1;
+    moe_item_range((long long)a.totals[1] * a.parts, it0, it1);
+    int staged = -1;
+    for (long long it = it0; it < it1; ++it) {
+        const int chunk = (int)(it / a.parts), part = (int)(it - (long long)chunk * a.parts);
+        const int e = moe_expert_of(a.coff, a.E, chunk);
+        const int pair0 = a.poff[e] + (chunk - a.coff[e]) * kMoeMxTok;
+        __syncthreads();  // the previous item's waves are done with the fragments and results
+        if (chunk != staged) {
+            const uint4* src = a.xf + (size_t)chunk * steps * 64;
+            for (int i = tid; i < steps * 64; i += 256) frag[i] = src[i];
+            if (tid < kMoeMxTok) tok_e[tid] = a.xe[chunk * kMoeMxTok + tid];
+            __syncthreads();
+            staged = chunk;
+        }
+        const int row_lo = part * a.part_rows;
+        const int row_hi = row_lo + a.part_rows < a.rows ? row_lo + a.part_rows : a.rows;
+        const int te0 = tok_e[2 * g], te1 = tok_e[2 * g + 1];
+        f4v acc[2][2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[j][0] = acc[j][1] = f4v{0.f, 0.f, 0.f, 0.f};
+        moe_mx_walk<T, AL, 2>(a, e, row_lo, row_hi, frag, acc, [&](int tile) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int lr = tile * kMoeMxRows + 32 * w + 16 * h + n;  // row within the part
+                const float g0 = __builtin_amdgcn_ldexpf(acc[0][h][0] + acc[0][h][1], te0);
+                const float g1 = __builtin_amdgcn_ldexpf(acc[0][h][2] + acc[0][h][3], te1);
+                const float u0 = __builtin_amdgcn_ldexpf(acc[1][h][0] + acc[1][h][1], te0);
+                const float u1 = __builtin_amdgcn_ldexpf(acc[1][h][2] + acc[1][h][3], te1);
+                res[lr * kMoeMxTok + 2 * g] = moe_act(g0, u0);
+                res[lr * kMoeMxTok + 2 * g + 1] = moe_act(g1, u1);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[j][h] = f4v{0.f, 0.f, 0.f, 0.f};
+            }
+        });
+        __syncthreads();
+        // store the part's act rows and fold their largest finite |act| per token
+        const int nr = row_hi - row_lo;
+        const int t = tid & (kMoeMxTok - 1);
+        unsigned mx = 0u;
+        for (int i = tid; i < nr * kMoeMxTok; i += 256) {  // i % kMoeMxTok == t
+            const int lr = i / kMoeMxTok;
+            const float v = res[i];
+            a.Y[(unsigned long long)(pair0 + t) * a.rows + row_lo + lr] = v;
+            const float f = fabsf(v);
+            if (f <= 3.402823466e38f) mx = max(mx, __float_as_uint(f));
+        }
+        if (mx) atomicMax(&a.amax[pair0 + t], mx);
+    }
+}
+
+template <int T, bool AL>
+__global__ __launch_bounds__(256, 2) void moe_dn_kernel(const MoeMxArgs a) {
+    extern __shared__ float smem[];
+    uint4* frag = reinterpret_cast<uint4*>(smem);
+    float* res = smem + (size_t)a.cols * 8;  // [part_rows][kMoeMxTok]
+    __shared__ int tok_e[kMoeMxTok];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, n = lane & 15;
+    const int steps = a.cols >> 5;
+    long long it0, it1;
+    moe_item_range((long long)a.totals[1] * a.parts, it0, it1);
+    int staged = -1;
+    for (long long it = it0; it < it1; ++it) {
+        const int chunk = (int)(it / a.parts), part = (int)(it - (long long)chunk * a.parts);
+        const int e = moe_expert_of(a.coff, a.E, chunk);
+        const int pair0 = a.poff[e] + (chunk - a.coff[e]) * kMoeMxTok;
+        __syncthreads();  // the previous item's waves are done with the fragments and results
+        if (chunk != staged) {
+            const int count = steps * 4 * kMoeMxTok;
+            for (int idx = tid; idx < count; idx += 256) {
+                const int t = idx % kMoeMxTok, gg = (idx / kMoeMxTok) & 3, st = idx / (4 * kMoeMxTok);
+                const float* p = a.act + (unsigned long long)(pair0 + t) * a.cols + 32 * st + 8 * gg;
+                const float4 x0 = ld_x4(p), x1 = ld_x4(p + 4);
+                const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+                uint4 h, l;
+                split8(v, norm_exp(__uint_as_float(a.amax[pair0 + t])), h, l);
+                frag[(st * 4 + gg) * 16 + 2 * t] = h;
+                frag[(st * 4 + gg) * 16 + 2 * t + 1] = l;
+            }
+            if (tid < kMoeMxTok) tok_e[tid] = norm_exp(__uint_as_float(a.amax[pair0 + tid]));
+            __syncthreads();
+            staged = chunk;
+        }
+        const int row_lo = part * a.part_rows;
+        const int row_hi = row_lo + a.part_rows < a.rows ? row_lo + a.part_rows : a.rows;
+        const int te0 = tok_e[2 * g], te1 = tok_e[2 * g + 1];
+        f4v acc[1][2];
+        acc[0][0] = acc[0][1] = f4v{0.f, 0.f, 0.f, 0.f};
+        moe_mx_walk<T, AL, 1>(a, e, row_lo, row_hi, frag, acc, [&](int tile) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int lr = tile * kMoeMxRows + 32 * w + 16 * h + n;
+                res[lr * kMoeMxTok + 2 * g] = __builtin_amdgcn_ldexpf(acc[0][h][0] + acc[0][h][1], te0);
+                res[lr * kMoeMxTok + 2 * g + 1] = __builtin_amdgcn_ldexpf(acc[0][h][2] + acc[0][h][3], te1);
+                acc[0][h] = f4v{0.f, 0.f, 0.f, 0.f};
+            }
+        });
+        __syncthreads();
+        const int nr = row_hi - row_lo;
+        for (int i = tid; i < nr * kMoeMxTok; i += 256) {
+            const int lr = i / kMoeMxTok, t = i - lr * kMoeMxTok;
+            a.Y[(unsigned long long)(pair0 + t) * a.rows + row_lo + lr] = res[i];
+        }
+    }
+}
+
+// gate/up (gu) or down launch of one block format; grid workgroups.
+template <int T, bool AL>
+static hipError_t moe_mx_launch_t(const MoeMxArgs& a, bool gu, int grid, hipStream_t s) {
+    const size_t lds = (size_t)a.cols * 32 + (size_t)a.part_rows * kMoeMxTok * 4;
+    const void* fn = gu ? reinterpret_cast<const void*>(&moe_gu_kernel<T, AL>)
+                        : reinterpret_cast<const void*>(&moe_dn_kernel<T, AL>);
+    static const hipError_t attr_gu = hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_gu_kernel<T, AL>),
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                          kMoeMxMaxCols * 32 + kMoeMxMaxPart * kMoeMxTok * 4);
+    static const hipError_t attr_dn = hipFuncSetAttribute(reinterpret_cast<const void*>(&moe_dn_kernel<T, AL>),
+                                                          hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                          kMoeMxMaxCols * 32 + kMoeMxMaxPart * kMoeMxTok * 4);
+    if (attr_gu != hipSuccess) return attr_gu;
+    if (attr_dn != hipSuccess) return attr_dn;
+    (void)fn;
+    if (gu)
+        hipLaunchKernelGGL((moe_gu_kernel<T, AL>), dim3((unsigned)grid), dim3(256), lds, s, a);
+    else
+        hipLaunchKernelGGL((moe_dn_kernel<T, AL>), dim3((unsigned)grid), dim3(256), lds, s, a);
+    return hipGetLastError();
+}
+
+static hipError_t moe_mx_launch(int type, const MoeMxArgs& a, bool gu, bool al, int grid, hipStream_t s) {
+#define PYRITE_CASE(T)                                                                                     \
+    case T:                                                                                              \
+        return (al && Geo<T>::bpb % 4 == 0) ? moe_mx_launch_t<T, (Geo<T>::bpb % 4 == 0)>(a, gu, grid, s) \
+                                            : moe_mx_launch_t<T, false>(a, gu, grid, s);
+    switch (type) {
+        PYRITE_CASE(T_Q4_0) PYRITE_CASE(T_Q4_1) PYRITE_CASE(T_Q5_0) PYRITE_CASE(T_Q5_1)
+        PYRITE_CASE(T_Q8_0) PYRITE_CASE(T_Q8_1) PYRITE_CASE(T_Q2_K) PYRITE_CASE(T_Q3_K)
+        PYRITE_CASE(T_Q4_K) PYRITE_CASE(T_Q5_K) PYRITE_CASE(T_Q6_K) PYRITE_CASE(T_IQ4_NL)
+        PYRITE_CASE(T_IQ4_XS)
+    default: return hipErrorInvalidValue;
+    }
+#undef PYRITE_CASE
+}
+
 int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, size_t ldo, int* ids_out,
                    float* wts_out, size_t batch, hipStream_t stream) {
     g_moe_err = nullptr;
@@ -585,13 +928,26 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     if (!L.router || !L.gate || !L.up || !L.down || !X || !out) return -3;
     if (L.router_len != E * rr || L.gate_len != E * gs || L.up_len != E * us || L.down_len != E * ds) return -3;
     if (ldx < H || ldo < H || (reinterpret_cast<uintptr_t>(X) & 3u)) return -3;
+    // From 32 tokens on (about 2 per expert and more), the block formats run
+    // their experts on the matrix cores in chunks of kMoeMxTok tokens;
+    // otherwise the VALU expert kernels (measured faster at 8 tokens).
+    const bool x16 = ((reinterpret_cast<uintptr_t>(X) & 15u) == 0) && (ldx % 4 == 0);
+    const bool mfma = batch >= 32 && x16 && L.gate_type == L.up_type && mx_type_supported(L.gate_type) &&
+                      mx_type_supported(L.down_type) && H <= (size_t)kMoeMxMaxCols && I <= (size_t)kMoeMxMaxCols;
     // chunk width: tokens per expert chunk (weights are read once per chunk)
-    const int MB = batch == 1 ? 1 : batch <= 16 ? 2 : 4;
+    const int MB = mfma ? kMoeMxTok : batch == 1 ? 1 : batch <= 16 ? 2 : 4;
     const size_t max_pairs = batch * K + E * (size_t)(MB - 1);
 
     Carver c{nullptr};
+    const size_t max_chunks = mfma ? max_pairs / kMoeMxTok : 0;
+    uint4* xf = nullptr;
+    int* xe = nullptr;
+    unsigned* amax = nullptr;
     auto layout = [&](Carver& cv, double** logits, double** mags, int** ids, double** wts, MoePlan* p, float** xg,
                       float** g, float** u, float** act, float** yd) {
+        xf = cv.take<uint4>(max_chunks * (H / 32) * 64);
+        xe = cv.take<int>(max_chunks * kMoeMxTok);
+        amax = cv.take<unsigned>(mfma ? max_pairs : 0);
         *logits = cv.take<double>(batch * E);
         *mags = cv.take<double>(batch * E);
         *ids = cv.take<int>(batch * K);
@@ -655,8 +1011,62 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     ra.plan = plan;
     hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)batch), dim3(256), 0, stream, ra);
     if (hipGetLastError() != hipSuccess) return -4;
+    if (mfma) {
+        // 3. fragments of each chunk's tokens; 4. gate and up with silu(gate) * up;
+        // 5. down; 6. combine.  Contiguous item ranges over twice the CUs, row
+        // parts so that about two items per workgroup exist at the likely
+        // chunk count (one per distinct expert).
+        const int grid = 2 * dev_info().cus;
+        const size_t est_chunks = E < batch * K ? E : batch * K;
+        hipLaunchKernelGGL(moe_xfrag_kernel, dim3((unsigned)max_chunks), dim3(256), 0, stream, X,
+                           (unsigned long long)ldx, (int)H, plan.pair_tok, plan.coff, plan.poff, plan.totals, (int)E,
+                           xf, xe, amax);
+        if (hipGetLastError() != hipSuccess) return -4;
+        MoeMxArgs xa;
+        xa.coff = plan.coff;
+        xa.poff = plan.poff;
+        xa.totals = plan.totals;
+        xa.E = (int)E;
+        xa.xf = xf;
+        xa.xe = xe;
+        xa.amax = amax;
+        auto set_parts = [&](size_t rows) {
+            size_t parts = (2 * (size_t)grid + est_chunks - 1) / est_chunks;
+            size_t pr = (rows + parts - 1) / parts;
+            pr = (pr + kMoeMxRows - 1) / kMoeMxRows * kMoeMxRows;
+            if (pr > (size_t)kMoeMxMaxPart) pr = kMoeMxMaxPart;
+            xa.part_rows = (int)pr;
+            xa.parts = (int)((rows + pr - 1) / pr);
+        };
+        xa.W[0] = static_cast<const uint8_t*>(L.gate);
+        xa.W[1] = static_cast<const uint8_t*>(L.up);
+        xa.slice = gs;
+        xa.row_bytes = H / gg.bs * gg.bpb;
+        xa.rows = (int)I;
+        xa.cols = (int)H;
+        xa.act = nullptr;
+        xa.Y = act;
+        set_parts(I);
+        const bool al_gu2 = ((reinterpret_cast<uintptr_t>(L.gate) | reinterpret_cast<uintptr_t>(L.up)) & 3u) == 0;
+        if (moe_mx_launch(L.gate_type, xa, true, al_gu2, grid, stream) != hipSuccess) return -4;
+        xa.W[0] = xa.W[1] = static_cast<const uint8_t*>(L.down);
+        xa.slice = ds;
+        xa.row_bytes = I / gd.bs * gd.bpb;
+        xa.rows = (int)H;
+        xa.cols = (int)I;
+        xa.xf = nullptr;
+        xa.xe = nullptr;
+        xa.act = act;
+        xa.Y = yd;
+        set_parts(H);
+        if (moe_mx_launch(L.down_type, xa, false, (reinterpret_cast<uintptr_t>(L.down) & 3u) == 0, grid, stream) !=
+            hipSuccess)
+            return -4;
+        hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)batch), dim3(256), 0,
+                           stream, yd, (int)H, (int)K, plan.pos, wts, out, (unsigned long long)ldo);
+        return hipGetLastError() == hipSuccess ? 0 : -4;
+    }
     // 3. gather (unless the gate/up launch gathers while staging)
-    const bool x16 = ((reinterpret_cast<uintptr_t>(X) & 15u) == 0) && (ldx % 4 == 0);
     const bool fuse_in = x16 && moe_fused_ok(L.gate_type, MB, H) && moe_fused_ok(L.up_type, MB, H);
     const bool fuse_act = moe_fused_ok(L.down_type, MB, I);
     if (!fuse_in) {

@@ -78,7 +78,7 @@ def _check(orc, layer, host, xs, what):
     return ids
 
 
-@pytest.mark.parametrize("batch", [1, 5, 20])
+@pytest.mark.parametrize("batch", [1, 5, 20, 40, 90])
 def test_moe_small(orc, dev, batch):
     rng = np.random.default_rng(100 + batch)
     layer, host = _layer(orc, rng, 16, 256, 256, 4, seed=7 + batch)
@@ -94,11 +94,15 @@ def test_moe_weight_options(orc, dev, norm, scale):
     _check(orc, layer, host, xs, f"norm={norm} scale={scale}")
 
 
-def test_moe_other_types(orc, dev):
+@pytest.mark.parametrize("batch", [4, 48])
+def test_moe_other_types(orc, dev, batch):
+    """Q5_K gate and up, Q3_K down (VALU experts at 4 tokens, matrix-core experts at 48);
+    mixed gate/up types keep the VALU experts."""
     rng = np.random.default_rng(300)
-    layer, host = _layer(orc, rng, 16, 512, 256, 4, types=(0, 13, 23, 11), seed=31)
-    xs = np.stack([orc.normal(700 + b, 512) for b in range(4)])
-    _check(orc, layer, host, xs, "Q5_K/IQ4_XS/Q3_K")
+    for types in ((0, 13, 13, 11), (0, 13, 23, 11), (0, 8, 8, 2)):
+        layer, host = _layer(orc, rng, 16, 512, 256, 4, types=types, seed=31)
+        xs = np.stack([orc.normal(700 + b, 512) for b in range(batch)])
+        _check(orc, layer, host, xs, f"types {types}")
 
 
 def test_moe_router_ties(orc, dev):
