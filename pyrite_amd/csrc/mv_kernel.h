@@ -111,6 +111,19 @@ struct MvGroup {
     MvDesc d[kMaxGroup];
 };
 
+// An empty use of every register of a loaded unit: the compiler must wait for
+// the unit's loads before it, on every path that reaches it.
+template <int R, class Raw>
+__device__ __forceinline__ void consume(const Raw (&raw)[R]) {
+    static_assert(sizeof(Raw) % 4 == 0, "units are whole dwords");
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const uint32_t* w = reinterpret_cast<const uint32_t*>(&raw[r]);
+#pragma unroll
+        for (int i = 0; i < (int)(sizeof(Raw) / 4); ++i) asm volatile("" ::"v"(w[i]));
+    }
+}
+
 // XL: activations staged in LDS (padded, see XView) instead of read from
 // global memory by every unit; used when B * cols fits the LDS budget.
 // BD: also accumulate each row's magnitude sum (Unit::bound, or sum |w||x| for
@@ -125,7 +138,9 @@ __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* sm
     const unsigned long long ldx = d.ldx;
     const int n16 = cols >> 4;
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // wave (and so wrow0 and the loop exits) in scalar registers: the loop
+    // branches stay uniform instead of exec-masked
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int LPR = 1 << lpr_log2, nslot = 64 >> lpr_log2;
     const int slot = lane >> lpr_log2, li = lane & (LPR - 1);
     const long long rows_per_wg = (long long)kMvWaves * nslot * R;
@@ -264,10 +279,17 @@ __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* sm
             for (int r = 0; r < R; ++r) rpl[r] = adv ? rp_nxt[r] : rp_cur[r];
             load_item(nxt, rpl, un);
             if (u < U) dot_item(cur, u);
+            // Every path waits for cur's loads here (a no-op after a decode).
+            // Without it the path that skips the decode leaves them pending,
+            // and the compiler's merged wait at the loop top drains nxt too.
+            consume(cur);
             if (adv) {
                 flush(row0);
                 wrow0 += stride_rows;
-                if (wrow0 >= rows) return true;
+                if (wrow0 >= rows) {
+                    consume(nxt);  // likewise for the exit edge the loop shares with its latch
+                    return true;
+                }
                 row0 += stride_rows;
 #pragma unroll
                 for (int r = 0; r < R; ++r) rp_cur[r] = rp_nxt[r];

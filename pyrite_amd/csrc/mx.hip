@@ -199,14 +199,10 @@ __global__ __launch_bounds__(256, 2) void mx_kernel(const MxGroup grp) {
             wv[k] = make_uint4(v.x, v.y, v.z, v.w);
         }
 
-        // 3. park the weights and build the A fragments
+        // 3. build the A fragments, then park the weights: the activations
+        // were loaded first and arrive first, so the fragments are built
+        // while the weight loads are still in flight
         lds_barrier();  // the previous task's fragments, weights and partials are consumed
-#pragma unroll
-        for (int k = 0; k < WI; ++k) {
-            const int c = tid + 256 * k;
-            const int r = c / nch, col = c - r * nch;
-            if (r < 32) *reinterpret_cast<uint4*>(wlds + r * rs + 16 * col) = wv[k];
-        }
         if (stage) {
             // Each token is staged scaled by the power of two 2^-e that brings
             // its largest finite |x| into [2^14, 2^15) (see norm_exp); results
@@ -233,6 +229,12 @@ __global__ __launch_bounds__(256, 2) void mx_kernel(const MxGroup grp) {
             }
             staged_mi = mi;
             staged_kp = kp;
+        }
+#pragma unroll
+        for (int k = 0; k < WI; ++k) {
+            const int c = tid + 256 * k;
+            const int r = c / nch, col = c - r * nch;
+            if (r < 32) *reinterpret_cast<uint4*>(wlds + r * rs + 16 * col) = wv[k];
         }
         lds_barrier();
 
@@ -319,6 +321,19 @@ static MxPlanOut mx_plan(MxGroup& grp) {
         d.kpart_steps = bpp * F::STEPS;
         d.nch = mx_nch<T>(bpp);
         d.rs = mx_rs<T>(bpp);
+    }
+    // Matrices split over more K parts take the lower task numbers, so their
+    // workgroups start first: their last part also sums the parts, the
+    // longest chain of the launch.  (Each descriptor carries its own
+    // pointers; the order changes no result.)
+    for (int i = 1; i < grp.n; ++i)
+        for (int j = i; j > 0 && grp.d[j - 1].ksplit < grp.d[j].ksplit; --j) {
+            const MxDesc t = grp.d[j];
+            grp.d[j] = grp.d[j - 1];
+            grp.d[j - 1] = t;
+        }
+    for (int i = 0; i < grp.n; ++i) {
+        MxDesc& d = grp.d[i];
         d.task_begin = (int)out.tasks;
         out.tasks += (long long)d.ksplit * d.tiles;
         if (d.ksplit > 1) {
