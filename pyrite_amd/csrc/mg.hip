@@ -68,7 +68,7 @@ __global__ __launch_bounds__(256) void mg_kernel(const MgArgs a) {
     // staging role: token tl, column group xg (8 columns) of steps xs0 + 2k
     const int tl = tid & 31, xg = (tid >> 5) & 3, xs0 = tid >> 7;
     const bool tok_ok = tok0 + tl < a.batch;
-    const float* xrow = a.X + (unsigned long long)(tok_ok ? tok0 + tl : 0) * a.ldx + 8 * xg;
+    const float* xrow = a.X + (unsigned long long)(tok_ok ? tok0 + tl : 0) * a.ldx;
 
     f4v acc[kMgSub][2];
 #pragma unroll
@@ -93,7 +93,8 @@ __global__ __launch_bounds__(256) void mg_kernel(const MgArgs a) {
         for (int k = 0; k < XI; ++k) {
             const int st = xs0 + 2 * k;
             if (tok_ok && st < ns) {
-                const float4 u = ld_x4(xrow + 32 * (s0 + st)), v = ld_x4(xrow + 32 * (s0 + st) + 4);
+                const float* q = xrow + mx_col<F>(s0 + st, xg);
+                const float4 u = ld_x4(q), v = ld_x4(q + 4);
                 xv[k][0] = u.x; xv[k][1] = u.y; xv[k][2] = u.z; xv[k][3] = u.w;
                 xv[k][4] = v.x; xv[k][5] = v.y; xv[k][6] = v.z; xv[k][7] = v.w;
             } else {
@@ -141,11 +142,14 @@ __global__ __launch_bounds__(256) void mg_kernel(const MgArgs a) {
 #pragma unroll
                 for (int p = 0; p < F::NACC; ++p) D[s][0][p] = D[s][1][p] = f4v{0.f, 0.f, 0.f, 0.f};
             const uint4* fb = frag + (size_t)(b - b0) * F::STEPS * 4 * 64;
+            typename MxPreOf<F>::type pa, pb;
+            mx_prep<F>(ca, g, pa);
+            mx_prep<F>(cb, g, pb);
 #pragma unroll
             for (int st = 0; st < F::STEPS; ++st) {
                 uint32_t ba[F::NACC][4], bb[F::NACC][4];
-                F::frag(ca, st, g, ba);
-                F::frag(cb, st, g, bb);
+                mx_frag<F>(ca, pa, st, g, ba);
+                mx_frag<F>(cb, pb, st, g, bb);
 #pragma unroll
                 for (int s = 0; s < kMgSub; ++s) {
                     const uint4 av = fb[(st * 4 + g) * 64 + s * 16 + n];

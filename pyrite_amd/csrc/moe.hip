@@ -579,7 +579,8 @@ static bool moe_fused_ok(int type, int MB, size_t cols) {
 // scaled by the power of two 2^-e_t that brings its largest finite |x| into
 // [2^14, 2^15), the results multiplied back by 2^e_t).
 //   moe_xfrag_kernel  one workgroup per chunk: gathers the chunk's tokens and
-//                     writes their A fragments and exponents once
+//                     writes their A fragments (in the gate/up format's
+//                     K-slot map) and exponents once
 //   moe_gu_kernel     items (chunk, row part): gate and up rows of the part
 //                     against the chunk's fragments (copied to LDS), writes
 //                     silu(gate) * up and the pair's largest finite |act|
@@ -629,7 +630,7 @@ __device__ __forceinline__ int moe_expert_of(const int* coff, int E, int chunk) 
 // chunk's act maxima cleared for moe_gu_kernel.
 __global__ __launch_bounds__(256) void moe_xfrag_kernel(const float* X, unsigned long long ldx, int cols,
                                                         const int* pair_tok, const int* coff, const int* poff,
-                                                        const int* totals, int E, uint4* xf, int* xe,
+                                                        const int* totals, int E, int kmode, uint4* xf, int* xe,
                                                         unsigned* amax) {
     __shared__ unsigned tok_max[kMoeMxTok];
     const int chunk = blockIdx.x;
@@ -653,7 +654,7 @@ __global__ __launch_bounds__(256) void moe_xfrag_kernel(const float* X, unsigned
             for (int i = 0; i < 8; ++i) v[i] = 0.f;
             return;
         }
-        const float* p = X + (unsigned long long)tok * ldx + 32 * st + 8 * gg;
+        const float* p = X + (unsigned long long)tok * ldx + mx_kcol(kmode, st, gg);
         const float4 x0 = ld_x4(p), x1 = ld_x4(p + 4);
         v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
     };
@@ -720,14 +721,17 @@ __device__ __forceinline__ void moe_mx_walk(const MoeMxArgs& a, int e, int row_l
 #pragma unroll
                 for (int c = 0; c < F::NACC; ++c) D[0][c] = D[1][c] = f4v{0.f, 0.f, 0.f, 0.f};
                 const uint4* fb = frag + (size_t)b * F::STEPS * 4 * 16;
+                typename MxPreOf<F>::type pa, pb;
+                mx_prep<F>(ra[p], g, pa);
+                mx_prep<F>(rb[p], g, pb);
 #pragma unroll
                 for (int st = 0; st < F::STEPS; ++st) {
                     const uint4 av = fb[(st * 4 + g) * 16 + n];
                     const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
                     const h8v A = __builtin_bit_cast(h8v, aw);
                     uint32_t ba[F::NACC][4], bb[F::NACC][4];
-                    F::frag(ra[p], st, g, ba);
-                    F::frag(rb[p], st, g, bb);
+                    mx_frag<F>(ra[p], pa, st, g, ba);
+                    mx_frag<F>(rb[p], pb, st, g, bb);
 #pragma unroll
                     for (int c = 0; c < F::NACC; ++c) {
                         D[0][c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8v, ba[c]), D[0][c], 0, 0, 0);
@@ -841,7 +845,7 @@ __global__ __launch_bounds__(256, 2) void moe_dn_kernel(const MoeMxArgs a) {
             const int count = steps * 4 * kMoeMxTok;
             for (int idx = tid; idx < count; idx += 256) {
                 const int t = idx % kMoeMxTok, gg = (idx / kMoeMxTok) & 3, st = idx / (4 * kMoeMxTok);
-                const float* p = a.act + (unsigned long long)(pair0 + t) * a.cols + 32 * st + 8 * gg;
+                const float* p = a.act + (unsigned long long)(pair0 + t) * a.cols + mx_col<Mx<T>>(st, gg);
                 const float4 x0 = ld_x4(p), x1 = ld_x4(p + 4);
                 const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
                 uint4 h, l;
@@ -896,6 +900,20 @@ static hipError_t moe_mx_launch_t(const MoeMxArgs& a, bool gu, int grid, hipStre
     else
         hipLaunchKernelGGL((moe_dn_kernel<T, AL>), dim3((unsigned)grid), dim3(256), lds, s, a);
     return hipGetLastError();
+}
+
+// K-slot map of a block format's MFMA fragments (mx_kcol)
+static int moe_kmode(int type) {
+#define PYRITE_CASE(T) \
+    case T: return MxKMode<Mx<T>>::value;
+    switch (type) {
+        PYRITE_CASE(T_Q4_0) PYRITE_CASE(T_Q4_1) PYRITE_CASE(T_Q5_0) PYRITE_CASE(T_Q5_1)
+        PYRITE_CASE(T_Q8_0) PYRITE_CASE(T_Q8_1) PYRITE_CASE(T_Q2_K) PYRITE_CASE(T_Q3_K)
+        PYRITE_CASE(T_Q4_K) PYRITE_CASE(T_Q5_K) PYRITE_CASE(T_Q6_K) PYRITE_CASE(T_IQ4_NL)
+        PYRITE_CASE(T_IQ4_XS)
+    default: return 0;
+    }
+#undef PYRITE_CASE
 }
 
 static hipError_t moe_mx_launch(int type, const MoeMxArgs& a, bool gu, bool al, int grid, hipStream_t s) {
@@ -1020,7 +1038,7 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
         const size_t est_chunks = E < batch * K ? E : batch * K;
         hipLaunchKernelGGL(moe_xfrag_kernel, dim3((unsigned)max_chunks), dim3(256), 0, stream, X,
                            (unsigned long long)ldx, (int)H, plan.pair_tok, plan.coff, plan.poff, plan.totals, (int)E,
-                           xf, xe, amax);
+                           moe_kmode(L.gate_type), xf, xe, amax);
         if (hipGetLastError() != hipSuccess) return -4;
         MoeMxArgs xa;
         xa.coff = plan.coff;

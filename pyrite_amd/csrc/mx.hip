@@ -98,6 +98,9 @@ __device__ __forceinline__ void mx_block(const typename Mx<T>::Raw& ra, const ty
         Da[p] = f4v{0.f, 0.f, 0.f, 0.f};
         Db[p] = f4v{0.f, 0.f, 0.f, 0.f};
     }
+    typename MxPreOf<F>::type pa, pb;
+    mx_prep<F>(ra, g, pa);
+    mx_prep<F>(rb, g, pb);
 #pragma unroll
     for (int st = 0; st < F::STEPS; ++st) {
         uint4 av = make_uint4(0u, 0u, 0u, 0u);
@@ -105,8 +108,8 @@ __device__ __forceinline__ void mx_block(const typename Mx<T>::Raw& ra, const ty
         const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
         const h8v a = __builtin_bit_cast(h8v, aw);
         uint32_t ba[F::NACC][4], bb[F::NACC][4];
-        F::frag(ra, st, g, ba);
-        F::frag(rb, st, g, bb);
+        mx_frag<F>(ra, pa, st, g, ba);
+        mx_frag<F>(rb, pb, st, g, bb);
 #pragma unroll
         for (int p = 0; p < F::NACC; ++p) {
             Da[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, __builtin_bit_cast(h8v, ba[p]), Da[p], 0, 0, 0);
@@ -157,12 +160,13 @@ __global__ __launch_bounds__(256, 2) void mx_kernel(const MxGroup grp) {
         float xv[XI][8];
         if (stage) {
             const bool tok_ok = xt < d.batch;
-            const float* xp = d.X + (unsigned long long)(tok_ok ? xt : 0) * d.ldx + 8 * xg;
+            const float* xp = d.X + (unsigned long long)(tok_ok ? xt : 0) * d.ldx;
 #pragma unroll
             for (int k = 0; k < XI; ++k) {
                 const int s = s0 + xs + SPI * k;
                 if (tok_ok && s < s1) {
-                    const float4 u = ld_x4(xp + 32 * s), v = ld_x4(xp + 32 * s + 4);
+                    const float* q = xp + mx_col<F>(s, xg);
+                    const float4 u = ld_x4(q), v = ld_x4(q + 4);
                     xv[k][0] = u.x; xv[k][1] = u.y; xv[k][2] = u.z; xv[k][3] = u.w;
                     xv[k][4] = v.x; xv[k][5] = v.y; xv[k][6] = v.z; xv[k][7] = v.w;
                 } else {

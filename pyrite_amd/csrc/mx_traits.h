@@ -26,6 +26,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace pyrite {
@@ -136,6 +138,21 @@ __device__ __forceinline__ void ld8(const uint8_t* p, uint32_t& a, uint32_t& b) 
     b = w[1];
 }
 
+// ---------------------------------------------------------------- K-slot maps
+// Which 8 columns the K-slots of lane group g hold in step S (counted from the
+// start of the row, 32 columns per step).  The A fragments (activations) are
+// staged with the same map as the B fragments (weights) use, so the products
+// pair up whatever the order: a dot product does not depend on the order of
+// its terms' positions in K.
+//   mode 0: columns 32 S + 8 g (step S = 32 consecutive columns);
+//   mode 1: 256-column blocks, lane group g owns columns 64 g .. 64 g + 63 of
+//           each block: 256 (S / 8) + 64 g + 8 (S % 8).  A lane then meets
+//           two 32-column sub-blocks per block instead of eight, so their
+//           scales are converted once per block.
+__device__ __forceinline__ int mx_kcol(int mode, int S, int g) {
+    return mode == 1 ? 256 * (S >> 3) + 64 * g + 8 * (S & 7) : 32 * S + 8 * g;
+}
+
 // ---------------------------------------------------------------- formats
 // Each format supplies:
 //   BS, BPB, STEPS (= BS / 32), NACC (1 or 2 accumulators per block)
@@ -143,21 +160,79 @@ __device__ __forceinline__ void ld8(const uint8_t* p, uint32_t& a, uint32_t& b) 
 //   load<AL>(blk, g, raw)
 //   frag(raw, step, g, b[NACC][4]): B fragments of one 32-column step
 //   epi(raw, D[NACC], acc): acc += block scale(s) applied to D
+// and optionally
+//   KMODE: its K-slot map (mx_kcol; 0 when absent)
+//   Pre, prep(raw, g, pre): per-block lane constants, after which the
+//   fragments are frag(raw, pre, step, g, b)
 template <int T> struct Mx;
 
+template <class F, class = void> struct MxKMode { static constexpr int value = 0; };
+template <class F> struct MxKMode<F, std::void_t<decltype(F::KMODE)>> { static constexpr int value = F::KMODE; };
+template <class F, class = void> struct MxHasPre : std::false_type {};
+template <class F> struct MxHasPre<F, std::void_t<typename F::Pre>> : std::true_type {};
+struct MxNoPre {};
+template <class F, bool = MxHasPre<F>::value> struct MxPreOf { using type = MxNoPre; };
+template <class F> struct MxPreOf<F, true> { using type = typename F::Pre; };
+
+// column of K-slot group g in step S of format F
+template <class F>
+__device__ __forceinline__ int mx_col(int S, int g) {
+    return mx_kcol(MxKMode<F>::value, S, g);
+}
+template <class F>
+__device__ __forceinline__ void mx_prep(const typename F::Raw& r, int g, typename MxPreOf<F>::type& p) {
+    if constexpr (MxHasPre<F>::value) F::prep(r, g, p);
+}
+template <class F>
+__device__ __forceinline__ void mx_frag(const typename F::Raw& r, const typename MxPreOf<F>::type& p, int st, int g,
+                                        uint32_t (&b)[F::NACC][4]) {
+    if constexpr (MxHasPre<F>::value) F::frag(r, p, st, g, b);
+    else F::frag(r, st, g, b);
+}
+
 // Q4_K: d | dmin | scales[12] | qs[128] (pyrite/kernels/native.c:173-197).
-// step j (sub-block j): columns 32j + l; j = 2c + h -> nibble h of qs[32c + l].
+// Sub-block j (columns 32j..32j+31, scale and min j): nibble j & 1 of
+// qs[32 (j >> 1) + l].  K-slot map 1: lane group g holds qs[32g..32g+31],
+// i.e. sub-blocks 2g (low nibbles, steps 0-3) and 2g + 1 (high nibbles,
+// steps 4-7); step s takes bytes 8 (s & 3)..+7 of them.
 template <> struct Mx<T_Q4_K> {
-    static constexpr int BS = 256, BPB = 144, STEPS = 8, NACC = 2;
-    struct Raw { uint32_t hd[4]; uint32_t q[4][2]; };
+    static constexpr int BS = 256, BPB = 144, STEPS = 8, NACC = 2, KMODE = 1;
+    struct Raw { uint32_t hd[4]; uint32_t q[8]; };
+    // packed (s, s), (-1024 s, -1024 s) and (m, m) halves of sub-blocks 2g, 2g + 1
+    struct Pre { uint32_t S[2], O[2], M[2]; };
     template <bool AL>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
         ld_span<16, AL>(b, r.hd);
-#pragma unroll
-        for (int c = 0; c < 4; ++c) ld8<AL>(b + 16 + 32 * c + 8 * g, r.q[c][0], r.q[c][1]);
+        ld_span<32, AL>(b + 16 + 32 * g, r.q);
     }
-    __device__ __forceinline__ static void scale_min(const Raw& r, int j, float& sc, float& mn) {
-        k4_scale_min(r.hd, j, sc, mn);
+    // scale and min of sub-block j, any j in 0..7 (get_scale_min_k4, native.c:52-61)
+    __device__ __forceinline__ static void k4_scale_min_rt(const uint32_t (&hd)[4], int j, uint32_t& a, uint32_t& m) {
+        const int sh = 8 * (j & 3);
+        const uint32_t s0 = hd[1] >> sh, s1 = hd[2] >> sh, s2 = hd[3] >> sh;
+        a = j < 4 ? (s0 & 63) : ((s2 & 15) | ((s0 >> 6 & 3) << 4));
+        m = j < 4 ? (s1 & 63) : ((s2 >> 4 & 15) | ((s1 >> 6 & 3) << 4));
+    }
+    __device__ __forceinline__ static void prep(const Raw& r, int g, Pre& p) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint32_t a, m;
+            k4_scale_min_rt(r.hd, 2 * g + h, a, m);
+            p.S[h] = splat_h((float)a);
+            p.O[h] = splat_h(-1024.f * (float)a);
+            p.M[h] = splat_h((float)m);
+        }
+    }
+    __device__ __forceinline__ static void frag(const Raw& r, const Pre& p, int s, int, uint32_t (&b)[2][4]) {
+        const int h = s >> 2, k = s & 3;
+        uint32_t x0 = r.q[2 * k], x1 = r.q[2 * k + 1];
+        if (h) { x0 >>= 4; x1 >>= 4; }
+        x0 &= 0x0F0F0F0Fu;
+        x1 &= 0x0F0F0F0Fu;
+        b[0][0] = pk_fma(bias_lo(x0), p.S[h], p.O[h]);
+        b[0][1] = pk_fma(bias_hi(x0), p.S[h], p.O[h]);
+        b[0][2] = pk_fma(bias_lo(x1), p.S[h], p.O[h]);
+        b[0][3] = pk_fma(bias_hi(x1), p.S[h], p.O[h]);
+        b[1][0] = b[1][1] = b[1][2] = b[1][3] = p.M[h];
     }
     __device__ __forceinline__ static void k4_scale_min(const uint32_t (&hd)[4], int j, float& sc, float& mn) {
         const uint32_t s0 = hd[1], s1 = hd[2], s2 = hd[3];
@@ -172,15 +247,6 @@ template <> struct Mx<T_Q4_K> {
         }
         sc = (float)a;
         mn = (float)m;
-    }
-    __device__ __forceinline__ static void frag(const Raw& r, int j, int, uint32_t (&b)[2][4]) {
-        const int c = j >> 1;
-        uint32_t x0 = r.q[c][0], x1 = r.q[c][1];
-        if (j & 1) { x0 >>= 4; x1 >>= 4; }
-        float sc, mn;
-        scale_min(r, j, sc, mn);
-        scaled8(x0 & 0x0F0F0F0Fu, x1 & 0x0F0F0F0Fu, sc, 0.f, b[0]);
-        splat8(mn, b[1]);
     }
     __device__ __forceinline__ static void epi(const Raw& r, const f4v (&D)[2], f4v& acc) {
         const float d = half_bits_to_float(r.hd[0]), dmin = half_bits_to_float(r.hd[0] >> 16);
