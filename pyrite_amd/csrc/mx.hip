@@ -66,7 +66,7 @@ constexpr unsigned kBufferWord3 = 0x00020000u;  // raw (untyped) buffer access o
 template <int T> constexpr int mx_nch(int nbp) { return (15 + nbp * Mx<T>::BPB + 15) / 16; }
 template <int T> constexpr int mx_rs(int nbp) { return 16 * (mx_nch<T>(nbp) | 1); }
 template <int T, int MB> constexpr bool mx_part_fits(int nbp) {
-    return nbp * Mx<T>::STEPS * MB * 64 + 32 * mx_rs<T>(nbp) <= kMxPartBudget &&
+    return nbp * Mx<T>::STEPS * MB * 64 + 32 * mx_rs<T>(nbp) + kMxLdsPad <= kMxPartBudget &&
            32 * mx_nch<T>(nbp) <= 256 * kMxMaxWLoads;
 }
 // largest part (in blocks) of this format at this fragment height
@@ -248,8 +248,8 @@ __global__ __launch_bounds__(256, 2) void mx_kernel(const MxGroup grp) {
         f4v acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
         for (int b = kb0 + w; b < kb1; b += 4) {
             typename F::Raw ra, rb;
-            F::template load<AL>(p0 + (b - kb0) * F::BPB, g, ra);
-            F::template load<AL>(p1 + (b - kb0) * F::BPB, g, rb);
+            F::template load<AL, true>(p0 + (b - kb0) * F::BPB, g, ra);
+            F::template load<AL, true>(p1 + (b - kb0) * F::BPB, g, rb);
             mx_block<T, MB>(ra, rb, frag + (b * F::STEPS - s0) * 4 * MB, g, n, acc);
         }
 
@@ -420,7 +420,7 @@ static hipError_t mx_launch_group(MxGroup& grp, hipStream_t stream, hipEvent_t s
     }
     const long long wgs = plan.tasks < kMxTargetWgs ? plan.tasks : kMxTargetWgs;
     grp.frag_bytes = plan.max_kps * 4 * MB * 16;
-    const size_t lds = kRedBytes + (size_t)grp.frag_bytes + (size_t)plan.max_wbytes;
+    const size_t lds = kRedBytes + (size_t)grp.frag_bytes + (size_t)plan.max_wbytes + kMxLdsPad;
     // more than 64 KiB of dynamic LDS: declare the kernel's largest need once
     static const hipError_t lds_ok = hipFuncSetAttribute(
         reinterpret_cast<const void*>(&mx_kernel<T, MB, AL>), hipFuncAttributeMaxDynamicSharedMemorySize,

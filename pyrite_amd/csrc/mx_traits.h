@@ -138,6 +138,39 @@ __device__ __forceinline__ void ld8(const uint8_t* p, uint32_t& a, uint32_t& b) 
     b = w[1];
 }
 
+// NB bytes at b + off in a copy of the weights in LDS (L; the MFMA matvec
+// stages them there): the dwords from there rounded down to 4 bytes, one byte
+// shift for the span (computed from b, so the spans of one block share it).
+// The dword after the span is read too; the LDS area ends with padding so
+// that it always exists.
+template <int NB>
+__device__ __forceinline__ void lds_span(const uint8_t* b, int off, uint32_t (&w)[(NB + 3) / 4]) {
+    constexpr int N = (NB + 3) / 4;
+    const uint32_t bs = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(b)) & 3u;
+    const uint32_t s = (bs + static_cast<uint32_t>(off)) & 3u;
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(b + off - s);
+    uint32_t t[N + 1];
+#pragma unroll
+    for (int k = 0; k <= N; ++k) t[k] = q[k];
+#pragma unroll
+    for (int k = 0; k < N; ++k) w[k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], s);
+}
+// the span reader of a format's load: global memory (ld_span) or LDS (L)
+template <int NB, bool AL, bool L>
+__device__ __forceinline__ void mx_span(const uint8_t* b, int off, uint32_t (&w)[(NB + 3) / 4]) {
+    if constexpr (L && !AL) lds_span<NB>(b, off, w);
+    else ld_span<NB, AL>(b + off, w);
+}
+template <bool AL, bool L>
+__device__ __forceinline__ void mx_ld8(const uint8_t* b, int off, uint32_t& x, uint32_t& y) {
+    uint32_t w[2];
+    mx_span<8, AL, L>(b, off, w);
+    x = w[0];
+    y = w[1];
+}
+// bytes of LDS padding after staged weights read with L
+constexpr int kMxLdsPad = 16;
+
 // ---------------------------------------------------------------- K-slot maps
 // Which 8 columns the K-slots of lane group g hold in step S (counted from the
 // start of the row, 32 columns per step).  The A fragments (activations) are
@@ -200,10 +233,10 @@ template <> struct Mx<T_Q4_K> {
     struct Raw { uint32_t hd[4]; uint32_t q[8]; };
     // packed (s, s), (-1024 s, -1024 s) and (m, m) halves of sub-blocks 2g, 2g + 1
     struct Pre { uint32_t S[2], O[2], M[2]; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_span<16, AL>(b, r.hd);
-        ld_span<32, AL>(b + 16 + 32 * g, r.q);
+        mx_span<16, AL, L>(b, 0, r.hd);
+        mx_span<32, AL, L>(b, 16 + 32 * g, r.q);
     }
     // scale and min of sub-block j, any j in 0..7 (get_scale_min_k4, native.c:52-61)
     __device__ __forceinline__ static void k4_scale_min_rt(const uint32_t (&hd)[4], int j, uint32_t& a, uint32_t& m) {
@@ -258,12 +291,12 @@ template <> struct Mx<T_Q4_K> {
 template <> struct Mx<T_Q5_K> {
     static constexpr int BS = 256, BPB = 176, STEPS = 8, NACC = 2;
     struct Raw { uint32_t hd[4]; uint32_t h[2]; uint32_t q[4][2]; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_span<16, AL>(b, r.hd);
-        ld8<AL>(b + 16 + 8 * g, r.h[0], r.h[1]);
+        mx_span<16, AL, L>(b, 0, r.hd);
+        mx_ld8<AL, L>(b, 16 + 8 * g, r.h[0], r.h[1]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) ld8<AL>(b + 48 + 32 * c + 8 * g, r.q[c][0], r.q[c][1]);
+        for (int c = 0; c < 4; ++c) mx_ld8<AL, L>(b, 48 + 32 * c + 8 * g, r.q[c][0], r.q[c][1]);
     }
     __device__ __forceinline__ static void frag(const Raw& r, int j, int, uint32_t (&b)[2][4]) {
         const int c = j >> 1;
@@ -289,15 +322,15 @@ template <> struct Mx<T_Q5_K> {
 template <> struct Mx<T_Q6_K> {
     static constexpr int BS = 256, BPB = 210, STEPS = 8, NACC = 2;
     struct Raw { uint32_t ql[4][2]; uint32_t qh[2][2]; uint32_t sc[4]; uint32_t d; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) ld8<AL>(b + 64 * (k >> 1) + 32 * (k & 1) + 8 * g, r.ql[k][0], r.ql[k][1]);
+        for (int k = 0; k < 4; ++k) mx_ld8<AL, L>(b, 64 * (k >> 1) + 32 * (k & 1) + 8 * g, r.ql[k][0], r.ql[k][1]);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) ld8<AL>(b + 128 + 32 * h + 8 * g, r.qh[h][0], r.qh[h][1]);
-        ld_span<16, AL>(b + 192, r.sc);
+        for (int h = 0; h < 2; ++h) mx_ld8<AL, L>(b, 128 + 32 * h + 8 * g, r.qh[h][0], r.qh[h][1]);
+        mx_span<16, AL, L>(b, 192, r.sc);
         uint32_t dd[1];
-        ld_span<2, AL>(b + 208, dd);
+        mx_span<2, AL, L>(b, 208, dd);
         r.d = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int s, int g, uint32_t (&b)[2][4]) {
@@ -325,14 +358,14 @@ template <> struct Mx<T_Q6_K> {
 template <> struct Mx<T_Q3_K> {
     static constexpr int BS = 256, BPB = 110, STEPS = 8, NACC = 1;
     struct Raw { uint32_t qs[2][2]; uint32_t hm[2]; uint32_t sc[3]; uint32_t d; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) ld8<AL>(b + 32 + 32 * h + 8 * g, r.qs[h][0], r.qs[h][1]);
-        ld8<AL>(b + 8 * g, r.hm[0], r.hm[1]);
-        ld_span<12, AL>(b + 96, r.sc);
+        for (int h = 0; h < 2; ++h) mx_ld8<AL, L>(b, 32 + 32 * h + 8 * g, r.qs[h][0], r.qs[h][1]);
+        mx_ld8<AL, L>(b, 8 * g, r.hm[0], r.hm[1]);
+        mx_span<12, AL, L>(b, 96, r.sc);
         uint32_t dd[1];
-        ld_span<2, AL>(b + 108, dd);
+        mx_span<2, AL, L>(b, 108, dd);
         r.d = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int s, int g, uint32_t (&b)[1][4]) {
@@ -359,13 +392,13 @@ template <> struct Mx<T_Q3_K> {
 template <> struct Mx<T_Q2_K> {
     static constexpr int BS = 256, BPB = 84, STEPS = 8, NACC = 2;
     struct Raw { uint32_t qs[2][2]; uint32_t sc[4]; uint32_t dd; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) ld8<AL>(b + 16 + 32 * h + 8 * g, r.qs[h][0], r.qs[h][1]);
-        ld_span<16, AL>(b, r.sc);
+        for (int h = 0; h < 2; ++h) mx_ld8<AL, L>(b, 16 + 32 * h + 8 * g, r.qs[h][0], r.qs[h][1]);
+        mx_span<16, AL, L>(b, 0, r.sc);
         uint32_t dd[1];
-        ld_span<4, AL>(b + 80, dd);
+        mx_span<4, AL, L>(b, 80, dd);
         r.dd = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int s, int g, uint32_t (&b)[2][4]) {
@@ -388,11 +421,11 @@ template <> struct Mx<T_Q2_K> {
 template <> struct Mx<T_IQ4_XS> {
     static constexpr int BS = 256, BPB = 136, STEPS = 8, NACC = 2;
     struct Raw { uint32_t hd[2]; uint32_t q[8][2]; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_span<8, AL>(b, r.hd);
+        mx_span<8, AL, L>(b, 0, r.hd);
 #pragma unroll
-        for (int ib = 0; ib < 8; ++ib) ld8<AL>(b + 8 + 16 * ib + 8 * (g & 1), r.q[ib][0], r.q[ib][1]);
+        for (int ib = 0; ib < 8; ++ib) mx_ld8<AL, L>(b, 8 + 16 * ib + 8 * (g & 1), r.q[ib][0], r.q[ib][1]);
     }
     __device__ __forceinline__ static void frag(const Raw& r, int ib, int g, uint32_t (&b)[2][4]) {
         uint32_t x0 = r.q[ib][0], x1 = r.q[ib][1];
@@ -412,9 +445,9 @@ template <> struct Mx<T_IQ4_XS> {
 
 // 32-element blocks: one step per block; lane group g owns columns 8g..8g+7,
 // the low nibbles of qs[8g..] for g < 2 and the high nibbles of qs[8(g-2)..].
-template <int OFF, int NB, bool AL>
+template <int OFF, int NB, bool AL, bool L>
 __device__ __forceinline__ void ld_nib8(const uint8_t* b, int g, uint32_t& x0, uint32_t& x1) {
-    ld8<AL>(b + OFF + 8 * (g & 1), x0, x1);
+    mx_ld8<AL, L>(b, OFF + 8 * (g & 1), x0, x1);
     if (g & 2) { x0 >>= 4; x1 >>= 4; }
     x0 &= 0x0F0F0F0Fu;
     x1 &= 0x0F0F0F0Fu;
@@ -424,11 +457,11 @@ __device__ __forceinline__ void ld_nib8(const uint8_t* b, int g, uint32_t& x0, u
 template <> struct Mx<T_Q4_0> {
     static constexpr int BS = 32, BPB = 18, STEPS = 1, NACC = 1;
     struct Raw { uint32_t x0, x1, d; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_nib8<2, 18, AL>(b, g, r.x0, r.x1);
+        ld_nib8<2, 18, AL, L>(b, g, r.x0, r.x1);
         uint32_t dd[1];
-        ld_span<2, AL>(b, dd);
+        mx_span<2, AL, L>(b, 0, dd);
         r.d = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int, int, uint32_t (&b)[1][4]) {
@@ -443,11 +476,11 @@ template <> struct Mx<T_Q4_0> {
 template <> struct Mx<T_IQ4_NL> {
     static constexpr int BS = 32, BPB = 18, STEPS = 1, NACC = 1;
     struct Raw { uint32_t x0, x1, d; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_nib8<2, 18, AL>(b, g, r.x0, r.x1);
+        ld_nib8<2, 18, AL, L>(b, g, r.x0, r.x1);
         uint32_t dd[1];
-        ld_span<2, AL>(b, dd);
+        mx_span<2, AL, L>(b, 0, dd);
         r.d = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int, int, uint32_t (&b)[1][4]) {
@@ -462,11 +495,11 @@ template <> struct Mx<T_IQ4_NL> {
 template <> struct Mx<T_Q4_1> {
     static constexpr int BS = 32, BPB = 20, STEPS = 1, NACC = 2;
     struct Raw { uint32_t x0, x1, dm; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_nib8<4, 20, AL>(b, g, r.x0, r.x1);
+        ld_nib8<4, 20, AL, L>(b, g, r.x0, r.x1);
         uint32_t dd[1];
-        ld_span<4, AL>(b, dd);
+        mx_span<4, AL, L>(b, 0, dd);
         r.dm = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int, int, uint32_t (&b)[2][4]) {
@@ -489,11 +522,11 @@ __device__ __forceinline__ void q5_high(uint32_t qh, int g, uint32_t& x0, uint32
 template <> struct Mx<T_Q5_0> {
     static constexpr int BS = 32, BPB = 22, STEPS = 1, NACC = 1;
     struct Raw { uint32_t x0, x1, d; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_nib8<6, 22, AL>(b, g, r.x0, r.x1);
+        ld_nib8<6, 22, AL, L>(b, g, r.x0, r.x1);
         uint32_t w[2];
-        ld_span<6, AL>(b, w);
+        mx_span<6, AL, L>(b, 0, w);
         r.d = w[0];
         q5_high(__builtin_amdgcn_alignbyte(w[1], w[0], 2u), g, r.x0, r.x1);
     }
@@ -509,11 +542,11 @@ template <> struct Mx<T_Q5_0> {
 template <> struct Mx<T_Q5_1> {
     static constexpr int BS = 32, BPB = 24, STEPS = 1, NACC = 2;
     struct Raw { uint32_t x0, x1, dm; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_nib8<8, 24, AL>(b, g, r.x0, r.x1);
+        ld_nib8<8, 24, AL, L>(b, g, r.x0, r.x1);
         uint32_t w[2];
-        ld_span<8, AL>(b, w);
+        mx_span<8, AL, L>(b, 0, w);
         r.dm = w[0];
         q5_high(w[1], g, r.x0, r.x1);
     }
@@ -532,11 +565,11 @@ template <int OFF, int NB>
 struct MxQ8 {
     static constexpr int BS = 32, BPB = NB, STEPS = 1, NACC = 1;
     struct Raw { uint32_t x0, x1, d; };
-    template <bool AL>
+    template <bool AL, bool L = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld8<AL>(b + OFF + 8 * g, r.x0, r.x1);
+        mx_ld8<AL, L>(b, OFF + 8 * g, r.x0, r.x1);
         uint32_t dd[1];
-        ld_span<2, AL>(b, dd);
+        mx_span<2, AL, L>(b, 0, dd);
         r.d = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int, int, uint32_t (&b)[1][4]) {
