@@ -6,7 +6,7 @@
 // pyrite_matvec (pyrite/kernels/native.c:518-555) with fp32 instead of fp64
 // arithmetic and a different summation order.
 //
-// Work decomposition: a workgroup is 4 wave64s.  A wave is split into
+// Work decomposition: a workgroup is 4 (or 8, 16) wave64s.  A wave is split into
 // 64/LPR row slots of LPR lanes (LPR = lanes per row, a power of two chosen so
 // a row's units fill it); each slot owns R consecutive rows and its lanes
 // stride over the units of those rows (a unit = one block, or a quarter of a
@@ -102,8 +102,8 @@ struct XSwiglu {
 
 constexpr int kMaxGroup = 16;
 
-// Workgroup shape: 4 waves.  (16-wave workgroups, which stage the
-// activations once per CU, measured slower: fewer waves fit per SIMD.)
+// Workgroup shape: 4 waves, or 8-16 where the staged activations would limit
+// the workgroups per CU (see launch_group_r).
 constexpr int kMvWaves = 4;
 constexpr int kMvThreads = 64 * kMvWaves;
 struct MvGroup {
@@ -128,7 +128,7 @@ __device__ __forceinline__ void consume(const Raw (&raw)[R]) {
 // global memory by every unit; used when B * cols fits the LDS budget.
 // BD: also accumulate each row's magnitude sum (Unit::bound, or sum |w||x| for
 // plain types) and store it to d.Bnd.
-template <int T, int B, int R, bool AL, bool XL, bool BD, class XS = XDirect>
+template <int T, int B, int R, bool AL, bool XL, bool BD, class XS = XDirect, int NW = kMvWaves>
 __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* smem) {
     static_assert(XL || std::is_same<XS, XDirect>::value, "indirect activations need LDS staging");
     constexpr int BS = Geo<T>::bs, BPB = Geo<T>::bpb;
@@ -143,10 +143,10 @@ __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* sm
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int LPR = 1 << lpr_log2, nslot = 64 >> lpr_log2;
     const int slot = lane >> lpr_log2, li = lane & (LPR - 1);
-    const long long rows_per_wg = (long long)kMvWaves * nslot * R;
+    const long long rows_per_wg = (long long)NW * nslot * R;
     const long long wave_rows = (long long)nslot * R;
     const long long stride_rows = (long long)d.wg_count * rows_per_wg;  // rows between row groups of this workgroup
-    long long wrow0 = (wg * kMvWaves + wave) * wave_rows;                        // first row of this wave (wave-uniform)
+    long long wrow0 = (wg * NW + wave) * wave_rows;                       // first row of this wave (wave-uniform)
     long long row0 = wrow0 + (long long)slot * R;                         // first row of this lane's slot
 
     float acc[R][B], bacc[R][B];
@@ -339,12 +339,15 @@ __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* sm
     }
 }
 
-template <int T, int B, int R, bool AL, bool XL, bool BD>
-__global__ __launch_bounds__(kMvThreads) void mv_kernel(const MvGroup g) {
+// NW waves per workgroup: 4, or 8-16 for launches whose staged activations
+// would otherwise limit the workgroups per CU (long rows): then one copy of x
+// in LDS serves 8-16 waves.
+template <int T, int B, int R, bool AL, bool XL, bool BD, int NW = kMvWaves>
+__global__ __launch_bounds__(64 * NW) void mv_kernel(const MvGroup g) {
     extern __shared__ float smem[];
     int i = 0;
     while (i + 1 < g.n && (int)blockIdx.x >= g.d[i + 1].wg_begin) ++i;
-    mv_body<T, B, R, AL, XL, BD>(g.d[i], (long long)blockIdx.x - g.d[i].wg_begin, smem);
+    mv_body<T, B, R, AL, XL, BD, XDirect, NW>(g.d[i], (long long)blockIdx.x - g.d[i].wg_begin, smem);
 }
 
 // ---------------------------------------------------------------- launcher
@@ -385,16 +388,26 @@ static const DevInfo& dev_info() {
 }
 
 // Workgroups of one kernel instance resident per CU, from its register use.
-template <int T, int B, int R, bool AL, bool XL, bool BD>
+template <int T, int B, int R, bool AL, bool XL, bool BD, int NW = kMvWaves>
 static int wgs_per_cu_regs() {
     static const int n = [] {
         int v = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, mv_kernel<T, B, R, AL, XL, BD>, kMvThreads, 0) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, mv_kernel<T, B, R, AL, XL, BD, NW>, 64 * NW, 0) !=
+                hipSuccess ||
             v < 1)
             v = 1;
         return v;
     }();
     return n;
+}
+
+// PYRITE_MATVEC_WAVES=4 keeps every VALU launch on 4-wave workgroups.
+static int matvec_waves_env() {
+    static const int v = [] {
+        const char* e = getenv("PYRITE_MATVEC_WAVES");
+        return e ? atoi(e) : 0;
+    }();
+    return v;
 }
 
 // Optional tuning override of the units per lane (PYRITE_MATVEC_KU = 1, 2,
@@ -419,10 +432,10 @@ static int plan_lpr(long long U) {
     return log2_ceil(per_lane < 64 ? per_lane : 64);
 }
 
-template <int T, int B, int R, bool AL, bool XL, bool BD>
+template <int T, int B, int R, bool AL, bool XL, bool BD, int NW = kMvWaves>
 static long long resident_wgs(size_t lds) {
     const DevInfo& di = dev_info();
-    long long per_cu = wgs_per_cu_regs<T, B, R, AL, XL, BD>();
+    long long per_cu = wgs_per_cu_regs<T, B, R, AL, XL, BD, NW>();
     if (lds > 0 && (long long)(di.lds_per_cu / lds) < per_cu) per_cu = (long long)(di.lds_per_cu / lds);
     if (per_cu < 1) per_cu = 1;
     return per_cu * di.cus;
@@ -465,7 +478,7 @@ static MatShape mat_shape(int rows, int cols) {
 // Fill wg_begin / wg_count (lpr_log2 is already set) and return the total
 // number of workgroups (at most cap).  Each matrix gets workgroups in
 // proportion to its weight bytes, never more than it has row groups.
-static long long plan_group(MvGroup& g, int R, long long cap) {
+static long long plan_group(MvGroup& g, int R, long long cap, int nw = kMvWaves) {
     double total_bytes = 0;
     for (int i = 0; i < g.n; ++i) total_bytes += (double)g.d[i].rows * (double)g.d[i].row_bytes;
     long long wg = 0;
@@ -473,7 +486,7 @@ static long long plan_group(MvGroup& g, int R, long long cap) {
         const double frac = ((double)g.d[i].rows * (double)g.d[i].row_bytes) / (total_bytes > 0 ? total_bytes : 1.0);
         long long share = (long long)((double)cap * frac);
         if (share < 1) share = 1;
-        const long long rows_per_wg = (long long)kMvWaves * (64 >> g.d[i].lpr_log2) * R;
+        const long long rows_per_wg = (long long)nw * (64 >> g.d[i].lpr_log2) * R;
         const long long need = (g.d[i].rows + rows_per_wg - 1) / rows_per_wg;
         const long long cnt = need < share ? need : share;
         g.d[i].wg_begin = (int)wg;
@@ -490,16 +503,32 @@ struct LaunchEvents {
     hipEvent_t stop = nullptr;
 };
 
-template <int T, int B, int R, bool AL, bool XL, bool BD>
-static hipError_t launch_group_r(MvGroup g, size_t lds, hipStream_t stream, LaunchEvents ev) {
-    const long long wgs = plan_group(g, R, resident_wgs<T, B, R, AL, XL, BD>(lds));
+template <int T, int B, int R, bool AL, bool XL, bool BD, int NW>
+static hipError_t launch_group_w(MvGroup g, size_t lds, hipStream_t stream, LaunchEvents ev) {
+    const long long wgs = plan_group(g, R, resident_wgs<T, B, R, AL, XL, BD, NW>(lds), NW);
     if (wgs <= 0 || wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
     if (ev.start || ev.stop)
-        hipExtLaunchKernelGGL((mv_kernel<T, B, R, AL, XL, BD>), dim3((unsigned)wgs), dim3(kMvThreads), (uint32_t)lds,
+        hipExtLaunchKernelGGL((mv_kernel<T, B, R, AL, XL, BD, NW>), dim3((unsigned)wgs), dim3(64 * NW), (uint32_t)lds,
                               stream, ev.start, ev.stop, 0, g);
     else
-        hipLaunchKernelGGL((mv_kernel<T, B, R, AL, XL, BD>), dim3((unsigned)wgs), dim3(kMvThreads), lds, stream, g);
+        hipLaunchKernelGGL((mv_kernel<T, B, R, AL, XL, BD, NW>), dim3((unsigned)wgs), dim3(64 * NW), lds, stream, g);
     return hipGetLastError();
+}
+
+// Staged activations that hold a CU below the workgroups its registers allow
+// (long rows) switch batch-1 launches to 16-wave workgroups and batch-2
+// launches to 8-wave ones (16 waves would cap them at 128 VGPRs and spill).
+template <int T, int B, int R, bool AL, bool XL, bool BD>
+static hipError_t launch_group_r(MvGroup g, size_t lds, hipStream_t stream, LaunchEvents ev) {
+    if constexpr (XL && B <= 2 && !BD) {
+        constexpr int NW = B == 1 ? 16 : 8;
+        const DevInfo& di = dev_info();
+        const long long by_regs = wgs_per_cu_regs<T, B, R, AL, XL, BD>();
+        if (lds > 0 && (long long)(di.lds_per_cu / lds) < by_regs && lds <= di.lds_per_cu &&
+            matvec_waves_env() != 4 && wgs_per_cu_regs<T, B, R, AL, XL, BD, NW>() >= 1)
+            return launch_group_w<T, B, R, AL, XL, BD, NW>(g, lds, stream, ev);
+    }
+    return launch_group_w<T, B, R, AL, XL, BD, kMvWaves>(g, lds, stream, ev);
 }
 
 template <int T, int B, int R, bool AL, bool BD>
