@@ -159,14 +159,33 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     __syncthreads();
 
     // rank of every expert in (-logit, e) order (a total order: ranks are
-    // unique); the first n land in s_top
+    // unique); the first n land in s_top.  Up to 128 experts, two threads
+    // count each expert's rank over half of the others each.
+    __shared__ int s_rank[kMoeMaxE];
     auto rank_top = [&](int n) {
-        for (int e = tid; e < E; e += 256) {
-            const double le = s_l[e];
+        if (E <= 128) {  // block-uniform branch
+            const int e = tid & 127, h = tid >> 7;
+            const int j0 = h * ((E + 1) >> 1), j1 = h ? E : (E + 1) >> 1;
             int r = 0;
+            if (e < E) {
+                const double le = s_l[e];
 #pragma unroll 8
-            for (int j = 0; j < E; ++j) r += rank_before(s_l[j], j, le, e);
-            if (r < n) s_top[r] = e;
+                for (int j = j0; j < j1; ++j) r += rank_before(s_l[j], j, le, e);
+                if (h == 0) s_rank[e] = r;
+            }
+            __syncthreads();
+            if (e < E && h == 1) {
+                r += s_rank[e];
+                if (r < n) s_top[r] = e;
+            }
+        } else {
+            for (int e = tid; e < E; e += 256) {
+                const double le = s_l[e];
+                int r = 0;
+#pragma unroll 8
+                for (int j = 0; j < E; ++j) r += rank_before(s_l[j], j, le, e);
+                if (r < n) s_top[r] = e;
+            }
         }
         __syncthreads();
     };
@@ -176,14 +195,28 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     //    rows whose bounds are both zero are exact)
     const int kk = k + 1 <= E ? k + 1 : E;
     rank_top(kk);
-    for (int e = tid; e < E; e += 256) {
-        for (int q = 0; q < kk; ++q) {
-            const int i = s_top[q];
-            if (i == e) continue;
-            const double bb = s_b[i] + s_b[e];
-            if ((bb > 0 && fabs(s_l[i] - s_l[e]) <= bb * (1 + 0x1p-40)) || !isfinite(s_l[e]) || !isfinite(s_l[i])) {
-                s_mark[e] = 1;
-                s_mark[i] = 1;
+    {
+        // the top rows' logits and bounds gathered next to their ids, so the
+        // scan below reads them without a dependent lookup
+        __shared__ double s_tl[kMoeMaxK + 1], s_tb[kMoeMaxK + 1];
+        if (tid < kk) {
+            s_tl[tid] = s_l[s_top[tid]];
+            s_tb[tid] = s_b[s_top[tid]];
+        }
+        __syncthreads();
+        // up to 128 experts, two threads share each expert's top rows
+        const bool two = E <= 128;
+        const int e0 = two ? (tid & 127) : tid, q0 = two ? (tid >> 7) : 0, qs = two ? 2 : 1;
+        for (int e = e0; e < E; e += two ? E : 256) {
+            const double le = s_l[e], be = s_b[e];
+            const bool fe = isfinite(le);
+            for (int q = q0; q < kk; q += qs) {
+                const int i = s_top[q];
+                const double tl = s_tl[q], bb = s_tb[q] + be;
+                if (i != e && ((bb > 0 && fabs(tl - le) <= bb * (1 + 0x1p-40)) || !fe || !isfinite(tl))) {
+                    s_mark[e] = 1;
+                    s_mark[i] = 1;
+                }
             }
         }
     }
@@ -204,13 +237,8 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     // 3. softmax: peak, exp(l - peak) summed (tree order; the reference sums
     //    left to right, which moves the weights by fp64 rounding only), the
     //    chosen probabilities, renormalisation and scale
-    double peak = -INFINITY;
-    for (int e = tid; e < E; e += 256) peak = fmax(peak, s_l[e]);
-    for (int off = 32; off > 0; off >>= 1) peak = fmax(peak, __shfl_xor(peak, off, 64));
-    if (lane == 0) s_red[wave] = peak;
-    __syncthreads();
-    peak = fmax(fmax(s_red[0], s_red[1]), fmax(s_red[2], s_red[3]));
-    __syncthreads();
+    // the peak is the first-ranked logit (NaN ranks as -inf, last)
+    const double peak = s_l[s_top[0]];
     double tot = 0.0;
     for (int e = tid; e < E; e += 256) tot += exp(s_l[e] - peak);
     for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off, 64);
@@ -223,23 +251,28 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
         s_w[tid] = total <= 0.0 ? 1.0 / (double)E : exp(s_l[e] - peak) / total;
     }
     __syncthreads();
-    if (tid == 0) {
+    // slot q's weight: renormalised by the sum of the k probabilities taken
+    // in rank order (each slot's thread forms the same sum), then scaled
+    if (tid < k) {
+        const int q = tid;
         double tk = 0.0;
         if (a.norm_topk)
-            for (int q = 0; q < k; ++q) tk += s_w[q];
-        for (int q = 0; q < k; ++q) {
-            double w = s_w[q];
-            if (a.norm_topk && tk > 0) w = w / tk;
-            if (a.scale != 1.0) w = w * a.scale;
-            const unsigned long long o = (unsigned long long)t * k + q;
-            st_dev(a.ids + o, s_top[q]);
-            a.wts[o] = w;
-            if (a.ids_out) a.ids_out[o] = s_top[q];
-            if (a.wts_out) a.wts_out[o] = (float)w;
-        }
-        // a single token's workgroup is the last by definition (and keeps its ids in LDS)
-        s_last = a.batch == 1 ? 1 : (arrive_dev(a.arrive) == (unsigned)a.batch - 1);
+            for (int j = 0; j < k; ++j) tk += s_w[j];
+        double w = s_w[q];
+        if (a.norm_topk && tk > 0) w = w / tk;
+        if (a.scale != 1.0) w = w * a.scale;
+        const unsigned long long o = (unsigned long long)t * k + q;
+        st_dev(a.ids + o, s_top[q]);
+        a.wts[o] = w;
+        if (a.ids_out) a.ids_out[o] = s_top[q];
+        if (a.wts_out) a.wts_out[o] = (float)w;
     }
+    if (a.batch > 1) {
+        drain_dev();  // this token's ids have completed before its arrival
+        __syncthreads();
+    }
+    // a single token's workgroup is the last by definition (and keeps its ids in LDS)
+    if (tid == 0) s_last = a.batch == 1 ? 1 : (arrive_dev(a.arrive) == (unsigned)a.batch - 1);
     __syncthreads();
     if (!s_last) return;
 
