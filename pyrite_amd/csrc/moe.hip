@@ -22,7 +22,7 @@
 //                       the VALU matvec body on each, weights read once per
 //                       chunk; the gate/up launch gathers each chunk's tokens
 //                       while staging them, the down launch applies
-//                       silu(gate) * up (fp64 inside) while staging
+//                       silu(gate) * up (fp32) while staging
 //   moe_gather_kernel,  used instead when the staged activations would not
 //   moe_swiglu_kernel   fit the LDS budget
 //   moe_combine_kernel  out = sum of w * down-out in slot order (fp64 inside)
@@ -379,9 +379,7 @@ __global__ __launch_bounds__(256) void moe_swiglu_kernel(const float* __restrict
     const unsigned long long n = (unsigned long long)(totals[0] < max_pairs ? totals[0] : max_pairs) * I;
     for (unsigned long long i = (unsigned long long)blockIdx.x * 256 + threadIdx.x; i < n;
          i += (unsigned long long)gridDim.x * 256) {
-        const double g = G[i];
-        const double s = g > -60.0 ? g / (1.0 + exp(-g)) : 0.0;
-        A[i] = (float)(s * (double)Uu[i]);
+        A[i] = XSwiglu::act(G[i], Uu[i]);  // the same activation as the staged path
     }
 }
 
