@@ -155,11 +155,29 @@ __device__ __forceinline__ void lds_span(const uint8_t* b, int off, uint32_t (&w
 #pragma unroll
     for (int k = 0; k < N; ++k) w[k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], s);
 }
-// the span reader of a format's load: global memory (ld_span) or LDS (L)
+// NB bytes at b + off in global memory, any alignment: as lds_span (one
+// shift from b), but only dwords that overlap the span are read, so no read
+// leaves the page of the span's bytes: the dword after the first N is read
+// only when the span reaches into it, else the last of the N again.
+template <int NB>
+__device__ __forceinline__ void gl_span(const uint8_t* b, int off, uint32_t (&w)[(NB + 3) / 4]) {
+    constexpr int N = (NB + 3) / 4;
+    const uint32_t bs = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(b)) & 3u;
+    const uint32_t s = (bs + static_cast<uint32_t>(off)) & 3u;
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(b + off - s);
+    uint32_t t[N + 1];
+#pragma unroll
+    for (int k = 0; k < N; ++k) t[k] = q[k];
+    t[N] = q[s + NB > 4 * N ? N : N - 1];
+#pragma unroll
+    for (int k = 0; k < N; ++k) w[k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], s);
+}
+// the span reader of a format's load: global memory or LDS (L)
 template <int NB, bool AL, bool L>
 __device__ __forceinline__ void mx_span(const uint8_t* b, int off, uint32_t (&w)[(NB + 3) / 4]) {
-    if constexpr (L && !AL) lds_span<NB>(b, off, w);
-    else ld_span<NB, AL>(b + off, w);
+    if constexpr (AL) ld_span<NB, AL>(b + off, w);
+    else if constexpr (L) lds_span<NB>(b, off, w);
+    else gl_span<NB>(b, off, w);
 }
 template <bool AL, bool L>
 __device__ __forceinline__ void mx_ld8(const uint8_t* b, int off, uint32_t& x, uint32_t& y) {
