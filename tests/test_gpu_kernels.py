@@ -153,6 +153,16 @@ def test_device_matvec_edge_shapes(torch_dev, t, shape):
     _device_matvec_check(torch_dev, t, rows, cols, 1, seed=9000 + rows + t)
 
 
+# Long rows whose staged activations limit the workgroups per CU: batch-1
+# launches run 16-wave workgroups and batch-2 launches 8-wave ones; ragged
+# row counts leave partial row groups in the last workgroups.
+@pytest.mark.parametrize("rows,cols,batch", [(333, 6144, 2), (300, 7936, 2), (1000, 8192, 1), (77, 10240, 1)])
+@pytest.mark.parametrize("t", [2, 8, 12, 14, 23], ids=lambda t: TYPES[t][0])
+def test_device_matvec_long_rows(torch_dev, t, rows, cols, batch):
+    announce("device_matvec_long_rows", TYPES[t][0], rows, cols, batch)
+    _device_matvec_check(torch_dev, t, rows, cols, batch, seed=9500 + rows + t)
+
+
 # The type sweep over the Qwen3-0.6B decode projections at batch 1 and 8.
 SWEEP_TYPES = [2, 7, 8, 11, 13, 14, 23]  # Q4_0 Q5_1 Q8_0 Q3_K Q5_K Q6_K IQ4_XS
 PROJECTIONS = {"q": (2048, 1024), "k": (1024, 1024), "v": (1024, 1024), "o": (1024, 2048),
