@@ -122,6 +122,64 @@ def run_cpu_baseline(weights, np, budget_s: float):
                       f"single-vector calls) through pyrite_matvec, single thread, {dt:.1f} s"}
 
 
+def run_cpu_baseline_parallel(weights, np, budget_s: float, nthreads: int):
+    """The same sweep on all host cores: thread i runs every call of the sweep
+    on its own contiguous i-th share of each matrix's rows (the reference
+    function is reentrant and rows are independent), so the threads never
+    wait for each other; throughput = all threads' bytes over the wall time."""
+    import threading
+
+    from oracle.oracle import oracle, reference
+
+    impl = reference() or oracle()
+    rng = np.random.default_rng(SEED + 7)
+    xs = {cols: rng.standard_normal((8, cols)) for cols in {c for _, _, c in PROJECTIONS}}
+    calls = []
+    for _, t in SWEEP_TYPES:
+        for rows, cols, payload, _ in weights[t]:
+            rb = payload.nbytes // rows
+            for batch in BATCHES:
+                for b in range(batch):
+                    calls.append((t, payload, rb, xs[cols][b], rows, cols))
+    done = [0] * nthreads
+    passes = [0] * nthreads
+    errors = []
+    start = threading.Barrier(nthreads + 1)
+    deadline = [0.0]
+
+    def worker(i):
+        outs = {}
+        start.wait()
+        while True:
+            for t, payload, rb, x, rows, cols in calls:
+                r0, r1 = rows * i // nthreads, rows * (i + 1) // nthreads
+                if r1 <= r0:
+                    continue
+                out = outs.setdefault((rows, r1 - r0), np.zeros(r1 - r0, dtype=np.float64))
+                if impl.matvec_raw(t, payload[r0 * rb:r1 * rb], x, out, r1 - r0, cols) != 0:
+                    errors.append(t)
+                    return
+                done[i] += (r1 - r0) * rb
+            passes[i] += 1
+            if time.perf_counter() >= deadline[0]:
+                return
+
+    threads = [threading.Thread(target=worker, args=(i,)) for i in range(nthreads)]
+    for th in threads:
+        th.start()
+    t0 = time.perf_counter()
+    deadline[0] = t0 + budget_s
+    start.wait()
+    for th in threads:
+        th.join()
+    dt = time.perf_counter() - t0
+    if errors:
+        raise ValueError("pyrite_matvec failed")
+    return {"value": sum(done) / dt / 1e9, "unit": "GB/s", "cores": nthreads,
+            "sample": f"{min(passes)}-{max(passes)} pass(es) of the same sweep per thread, thread i on its "
+                      f"i-th share of every matrix's rows, {nthreads} threads, {dt:.1f} s"}
+
+
 # ---------------------------------------------------------------- other configurations
 # Each is timed as `reps` calls captured in one HIP graph (replayed once after
 # a warm-up replay), over rotated weight copies or varying inputs so that
@@ -474,6 +532,10 @@ def main() -> int:
         cpu = run_cpu_baseline(weights, np, args.cpu_seconds)
         model, ncpu = cpu_info()
         cpu["host"] = f"{model}, {ncpu} logical CPUs visible"
+        # all host cores (at most 16, the box's CPU share)
+        nthreads = max(1, min(16, ncpu))
+        log(f"cpu baseline on {nthreads} threads (~{args.cpu_seconds:.0f} s)")
+        cpu["all_cores"] = run_cpu_baseline_parallel(weights, np, args.cpu_seconds, nthreads)
 
     result = {
         "metric": "dequant-matvec GB/s on quantized bytes (% HBM peak); MoE-layer tokens/s at b=1/64",
