@@ -1063,8 +1063,9 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     if (mfma) {
         // 3. fragments of each chunk's tokens; 4. gate and up with silu(gate) * up;
         // 5. down; 6. combine.  Contiguous item ranges over twice the CUs, row
-        // parts so that about two items per workgroup exist at the likely
-        // chunk count (one per distinct expert).
+        // parts so that about one item per workgroup exists at the likely
+        // chunk count (one per distinct expert; measured on MI355X, fewer and
+        // larger items beat two or more per workgroup).
         const int grid = 2 * dev_info().cus;
         const size_t est_chunks = E < batch * K ? E : batch * K;
         hipLaunchKernelGGL(moe_xfrag_kernel, dim3((unsigned)max_chunks), dim3(256), 0, stream, X,
@@ -1080,7 +1081,7 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
         xa.xe = xe;
         xa.amax = amax;
         auto set_parts = [&](size_t rows) {
-            size_t parts = (2 * (size_t)grid + est_chunks - 1) / est_chunks;
+            size_t parts = ((size_t)grid + est_chunks - 1) / est_chunks;
             size_t pr = (rows + parts - 1) / parts;
             pr = (pr + kMoeMxRows - 1) / kMoeMxRows * kMoeMxRows;
             if (pr > (size_t)kMoeMxMaxPart) pr = kMoeMxMaxPart;
