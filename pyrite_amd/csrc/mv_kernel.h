@@ -568,15 +568,35 @@ static char matvec_path_env() {
     return c;
 }
 
-// Largest instantiated batch chunk (8, 4, 2, 1) not above `left` whose LDS
-// column sums fit 64 KiB; 0 if none.
-template <bool BD>
-static int valu_chunk(size_t left, bool quant, size_t max_cols) {
-    for (int cand : {8, 4, 2, 1}) {
-        if ((size_t)cand > left) continue;
-        if (!quant || (size_t)(BD ? 2 : 1) * cand * (max_cols / 16) * sizeof(float) <= 65536) return cand;
+// Largest instantiated batch chunk (8, 4, 2, 1) not above `left` whose
+// staged activations (column sums and the padded copy) fit 64 KiB; else the
+// largest whose column sums alone fit (activations then read from memory per
+// unit, which is slower than two launches that stage them: measured 45 vs
+// 2 x 17.5 us for a 4096 x 14336 Q6_K matrix at batch 2); 0 if none.
+template <int T, bool BD>
+static int valu_chunk_t(size_t left, size_t max_cols) {
+    if constexpr (Geo<T>::bs == 1) {
+        return left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+    } else {
+        if (left >= 8 && use_xl<T, 8, BD>((int)max_cols)) return 8;
+        if (left >= 4 && use_xl<T, 4, BD>((int)max_cols)) return 4;
+        if (left >= 2 && use_xl<T, 2, BD>((int)max_cols)) return 2;
+        if (use_xl<T, 1, BD>((int)max_cols)) return 1;
+        const size_t sums1 = (BD ? 2 : 1) * (max_cols / 16) * sizeof(float);
+        for (int cand : {8, 4, 2, 1})
+            if ((size_t)cand <= left && cand * sums1 <= 65536) return cand;
+        return 0;
     }
-    return 0;
+}
+template <bool BD>
+static int valu_chunk(int type, size_t left, size_t max_cols) {
+#define PYRITE_CASE(T) \
+    case T: return valu_chunk_t<T, BD>(left, max_cols);
+    switch (type) {
+        PYRITE_FOR_EACH_TYPE(PYRITE_CASE)
+    default: return 0;
+    }
+#undef PYRITE_CASE
 }
 
 // VALU launches over batch chunks and groups of kMaxGroup matrices; bnd
@@ -585,10 +605,9 @@ template <bool BD>
 static int valu_group_launch(int type, const TypeGeo& g, bool al, const MatvecArgs* mats, float* const* bnd,
                              size_t n, size_t batch, size_t max_cols, hipStream_t stream, hipEvent_t start,
                              hipEvent_t stop) {
-    const bool quant = g.bs > 1;
     size_t done = 0;
     while (done < batch) {
-        const int c = valu_chunk<BD>(batch - done, quant, max_cols);
+        const int c = valu_chunk<BD>(type, batch - done, max_cols);
         if (c == 0) return -2;
         for (size_t base = 0; base < n; base += kMaxGroup) {
             LaunchEvents ev;
