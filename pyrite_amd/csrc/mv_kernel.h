@@ -460,6 +460,15 @@ template <int T, int B, bool BD>
 static bool use_xl(int max_cols) {
     return Geo<T>::bs > 1 && lds_bytes<T, B, BD>(max_cols, true) <= 65536;
 }
+// The plain matvec also stages batch-1/2 activations of long rows in up to
+// kMvXlMax bytes of LDS (one 8- or 16-wave workgroup per CU; the launch
+// raises the kernel's dynamic LDS limit).
+constexpr int kMvXlMax = 144 * 1024;
+template <int T, int B, bool BD>
+static bool use_xl_mv(int max_cols) {
+    if (use_xl<T, B, BD>(max_cols)) return true;
+    return Geo<T>::bs > 1 && B <= 2 && !BD && lds_bytes<T, B, BD>(max_cols, true) <= (size_t)kMvXlMax;
+}
 
 // Slot shape of one matrix (rows per slot R, lanes per row), a function of
 // the matrix only, so a matrix gives bit-identical results whether it is
@@ -504,6 +513,12 @@ struct LaunchEvents {
 
 template <int T, int B, int R, bool AL, bool XL, bool BD, int NW>
 static hipError_t launch_group_w(MvGroup g, size_t lds, hipStream_t stream, LaunchEvents ev) {
+    if (lds > 65536) {
+        static const hipError_t attr =
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&mv_kernel<T, B, R, AL, XL, BD, NW>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, kMvXlMax);
+        if (attr != hipSuccess) return attr;
+    }
     const long long wgs = plan_group(g, R, resident_wgs<T, B, R, AL, XL, BD, NW>(lds), NW);
     if (wgs <= 0 || wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
     if (ev.start || ev.stop)
@@ -535,7 +550,7 @@ static hipError_t launch_group_rx(const MvGroup& g, hipStream_t stream, LaunchEv
     int max_cols = 0;
     for (int i = 0; i < g.n; ++i) max_cols = g.d[i].cols > max_cols ? g.d[i].cols : max_cols;
     if constexpr (Geo<T>::bs > 1) {
-        if (use_xl<T, B, BD>(max_cols))
+        if (use_xl_mv<T, B, BD>(max_cols))
             return launch_group_r<T, B, R, AL, true, BD>(g, lds_bytes<T, B, BD>(max_cols, true), stream, ev);
     }
     return launch_group_r<T, B, R, AL, false, BD>(g, lds_bytes<T, B, BD>(max_cols, false), stream, ev);
@@ -569,7 +584,7 @@ static char matvec_path_env() {
 }
 
 // Largest instantiated batch chunk (8, 4, 2, 1) not above `left` whose
-// staged activations (column sums and the padded copy) fit 64 KiB; else the
+// staged activations (column sums and the padded copy) fit LDS; else the
 // largest whose column sums alone fit (activations then read from memory per
 // unit, which is slower than two launches that stage them: measured 45 vs
 // 2 x 17.5 us for a 4096 x 14336 Q6_K matrix at batch 2); 0 if none.
@@ -578,10 +593,10 @@ static int valu_chunk_t(size_t left, size_t max_cols) {
     if constexpr (Geo<T>::bs == 1) {
         return left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
     } else {
-        if (left >= 8 && use_xl<T, 8, BD>((int)max_cols)) return 8;
-        if (left >= 4 && use_xl<T, 4, BD>((int)max_cols)) return 4;
-        if (left >= 2 && use_xl<T, 2, BD>((int)max_cols)) return 2;
-        if (use_xl<T, 1, BD>((int)max_cols)) return 1;
+        if (left >= 8 && use_xl_mv<T, 8, BD>((int)max_cols)) return 8;
+        if (left >= 4 && use_xl_mv<T, 4, BD>((int)max_cols)) return 4;
+        if (left >= 2 && use_xl_mv<T, 2, BD>((int)max_cols)) return 2;
+        if (use_xl_mv<T, 1, BD>((int)max_cols)) return 1;
         const size_t sums1 = (BD ? 2 : 1) * (max_cols / 16) * sizeof(float);
         for (int cand : {8, 4, 2, 1})
             if ((size_t)cand <= left && cand * sums1 <= 65536) return cand;

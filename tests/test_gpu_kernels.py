@@ -154,9 +154,11 @@ def test_device_matvec_edge_shapes(torch_dev, t, shape):
 
 
 # Long rows whose staged activations limit the workgroups per CU: batch-1
-# launches run 16-wave workgroups and batch-2 launches 8-wave ones; ragged
-# row counts leave partial row groups in the last workgroups.
-@pytest.mark.parametrize("rows,cols,batch", [(333, 6144, 2), (300, 7936, 2), (1000, 8192, 1), (77, 10240, 1)])
+# launches run 16-wave workgroups and batch-2 launches 8-wave ones, with more
+# than 64 KiB of LDS for the longest; ragged row counts leave partial row
+# groups in the last workgroups.
+@pytest.mark.parametrize("rows,cols,batch", [(333, 6144, 2), (300, 7936, 2), (1000, 8192, 1), (77, 10240, 1),
+                                               (129, 14336, 2), (65, 28672, 1)])
 @pytest.mark.parametrize("t", [2, 8, 12, 14, 23], ids=lambda t: TYPES[t][0])
 def test_device_matvec_long_rows(torch_dev, t, rows, cols, batch):
     announce("device_matvec_long_rows", TYPES[t][0], rows, cols, batch)
