@@ -127,6 +127,39 @@ def test_moe_router_ties(orc, dev):
     assert len(set(ids[0].tolist())) == 8
 
 
+def test_moe_repeat_and_graph(orc, dev):
+    """Back-to-back calls of two batch sizes and graph replays give identical
+    outputs: the routing kernel's arrival counter and the shared workspace
+    carry nothing from one call into the next."""
+    from pyrite_amd import device
+    rng = np.random.default_rng(900)
+    layer, host = _layer(orc, rng, 16, 256, 256, 4, seed=91)
+    xs = np.stack([orc.normal(900 + b, 256) for b in range(3)])
+    xa = torch.from_numpy(xs).to("cuda:0")
+    xb = xa[:1].clone()
+    announce("moe", "repeat + graph", "E=16", "H=256", "I=256", "k=4", "batch=3,1")
+    first_a = device.moe_ffn(layer, xa)[0].clone()
+    first_b = device.moe_ffn(layer, xb)[0].clone()
+    for _ in range(2):
+        assert torch.equal(device.moe_ffn(layer, xa)[0], first_a)
+        assert torch.equal(device.moe_ffn(layer, xb)[0], first_b)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    out = torch.empty_like(first_a)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        device.moe_ffn(layer, xa, out=out)
+    for _ in range(3):
+        out.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, first_a)
+        assert torch.equal(device.moe_ffn(layer, xb)[0], first_b)
+    torch.cuda.synchronize()
+    _check(orc, layer, host, xs, "repeat")
+
+
 def test_moe_qwen3_30b_shape(orc, dev):
     """Qwen3-30B-A3B MoE shape: 128 experts, hidden 2048, moe_intermediate 768, top-8."""
     rng = np.random.default_rng(20244)
