@@ -20,7 +20,7 @@ stream right after the timed replay.
 Prints one JSON line.  value = quantized weight bytes / second over the timed
 steps (GB/s).  --gpus N > 1 exits: this path runs on one GPU.
 
-The line also carries, under "configs", the other configurations of the
+The line also carries, under "workloads", the other workloads of the
 path, each timed as calls captured in one HIP graph: the single Q4_K
 3072x1024 matvec, the Q6_K 151936x1024 LM head with its exact greedy id, the
 Qwen3-30B-A3B MoE layer (tokens/s at batch 1, 8, 64) and the Llama-3-8B
@@ -246,7 +246,7 @@ def load_traffic(key: str):
     return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
-def bench_config1(torch, np, quantize, stream, device):
+def bench_q4k_single(torch, np, quantize, stream, device):
     """Single Q4_K 3072x1024 matvec (Qwen3-0.6B ffn_up), batch 1."""
     rows, cols = 3072, 1024
     p = quantized_normal(np, quantize, 12, rows * cols, SEED + 11)
@@ -378,13 +378,13 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extra", action="store_true", help="skip the LM-head, MoE and Llama configurations")
     ap.add_argument("--only", default=None,
-                    help="run only the named extra configuration (config1_q4k_3072x1024, config3_lm_head, "
-                         "config4_moe, config5_llama3_8b_layer, copy_calibration) and print its JSON; "
+                    help="run only the named extra configuration (q4k_3072x1024, lm_head_q6k_151936x1024, "
+                         "moe_qwen3_30b_a3b, llama3_8b_layer, copy_calibration) and print its JSON; "
                          "for profiling")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures the dequant-matvec path on one GPU; runs on more than one GPU "
-              "are not part of this build (--gpus must be 1)", file=sys.stderr)
+              "are not implemented (--gpus must be 1)", file=sys.stderr)
         return 2
 
     import numpy as np
@@ -401,10 +401,10 @@ def main() -> int:
         stream = torch.cuda.Stream()
         torch.cuda.set_stream(stream)
         sptr = ctypes.c_void_p(stream.cuda_stream)
-        fns = {"config1_q4k_3072x1024": lambda: bench_config1(torch, np, quantize, stream, device),
-               "config3_lm_head": lambda: bench_lm_head(torch, np, quantize, stream, device),
-               "config4_moe": lambda: bench_moe(torch, np, quantize, stream, device),
-               "config5_llama3_8b_layer": lambda: bench_llama(torch, np, quantize, stream, device, lib, sptr),
+        fns = {"q4k_3072x1024": lambda: bench_q4k_single(torch, np, quantize, stream, device),
+               "lm_head_q6k_151936x1024": lambda: bench_lm_head(torch, np, quantize, stream, device),
+               "moe_qwen3_30b_a3b": lambda: bench_moe(torch, np, quantize, stream, device),
+               "llama3_8b_layer": lambda: bench_llama(torch, np, quantize, stream, device, lib, sptr),
                "copy_calibration": lambda: copy_calibration(torch, stream)}
         print(json.dumps({args.only: fns[args.only]()}), flush=True)
         return 0
@@ -517,10 +517,10 @@ def main() -> int:
     if not args.no_extra:
         from pyrite_amd import device
         extra = {}
-        for name, fn in (("config1_q4k_3072x1024", lambda: bench_config1(torch, np, quantize, stream, device)),
-                         ("config3_lm_head", lambda: bench_lm_head(torch, np, quantize, stream, device)),
-                         ("config4_moe", lambda: bench_moe(torch, np, quantize, stream, device)),
-                         ("config5_llama3_8b_layer", lambda: bench_llama(torch, np, quantize, stream, device, lib,
+        for name, fn in (("q4k_3072x1024", lambda: bench_q4k_single(torch, np, quantize, stream, device)),
+                         ("lm_head_q6k_151936x1024", lambda: bench_lm_head(torch, np, quantize, stream, device)),
+                         ("moe_qwen3_30b_a3b", lambda: bench_moe(torch, np, quantize, stream, device)),
+                         ("llama3_8b_layer", lambda: bench_llama(torch, np, quantize, stream, device, lib,
                                                                          sptr))):
             log(f"extra configuration: {name}")
             extra[name] = fn()
@@ -560,7 +560,7 @@ def main() -> int:
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "configs": extra,
+        "workloads": extra,
         "per_kernel": {k: {kk: round(vv, 3) if isinstance(vv, float) else vv for kk, vv in v.items()}
                        for k, v in sorted(per_kernel.items())},
     }

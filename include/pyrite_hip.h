@@ -4,7 +4,7 @@
  * Part 1 is a drop-in for the reference's native kernel library: the same three
  * symbols, signatures, argument meaning and return codes as
  * pyrite/kernels/native.c, so pyrite/kernels/native.py can load this library
- * instead of compiling native.c (see INTEGRATION.md for the binding).
+ * instead of compiling native.c (one extra branch in its _load_library).
  *
  * Part 2 is device-resident: weights are GGUF block bytes uploaded verbatim
  * into HBM, activations and outputs are fp32 device buffers, and work is

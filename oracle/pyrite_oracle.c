@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the fused GGML dequantize x matvec hot path.
  *
- * TEST INFRASTRUCTURE ONLY: the checker the HIP kernels are compared against,
+ * TEST INFRASTRUCTURE ONLY: the reference the HIP kernels are compared against,
  * never the thing measured or shipped.  Build flags (oracle/Makefile) keep
  * IEEE double semantics: no fast-math and no FMA contraction, so every
  * rounding happens where the C source says, exactly as in the reference build

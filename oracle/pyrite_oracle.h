@@ -5,7 +5,7 @@
  * double arithmetic, what the reference computes on this path so that the
  * HIP kernels can be checked against it.  Only tests/, the smoke check in
  * __graft_entry__.py and the cpu_baseline leg of bench.py may load it, and
- * only as the checker: the product library (pyrite_amd) never calls it and
+ * only to compare against: the product library (pyrite_amd) never calls it and
  * has no CPU fallback.
  *
  * Every function names the reference file:line it follows.  Reference paths

@@ -181,7 +181,7 @@ def test_qwen3_projection_sweep(torch_dev, t, batch):
 
 def test_q4_k_config_one(torch_dev):
     """Q4_K 3072 x 1024 from N(0, 0.02), x N(0, 1), batch 1."""
-    announce("config1 q4_k 3072x1024")
+    announce("q4_k 3072x1024 (Qwen3-0.6B ffn_up)")
     _device_matvec_check(torch_dev, 12, 3072, 1024, 1, seed=20241001)
 
 

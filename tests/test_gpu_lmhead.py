@@ -168,7 +168,7 @@ def test_lm_head_nonfinite_activation(orc, dev):
     _check(orc, dev, t, payload, rows, cols, x[None, :], "inf-x")
 
 
-def test_lm_head_config3_full_vocab(orc, dev):
+def test_lm_head_full_vocab_151936(orc, dev):
     """The Qwen3 LM-head shape: Q6_K 151936 x 1024, RMS-normalised N(0, 1) input."""
     t, rows, cols = 14, 151936, 1024
     rng = np.random.default_rng(20243)
@@ -179,7 +179,7 @@ def test_lm_head_config3_full_vocab(orc, dev):
     payload = raw.reshape(-1)
     x = orc.normal(20243200, cols).astype(np.float64)
     x = (x / np.sqrt(np.mean(x * x) + 1e-6)).astype(np.float32)
-    _check(orc, dev, t, payload, rows, cols, x[None, :], "config3")
+    _check(orc, dev, t, payload, rows, cols, x[None, :], "vocab 151936")
 
 
 @pytest.mark.parametrize("n,batch", [(1024, 1), (2048, 3), (1000, 2)])
