@@ -11,6 +11,11 @@
  * queued on a caller-supplied HIP stream (NULL = the per-thread default
  * stream).  These replace the per-call host round trips at the reference's
  * dispatch sites (pyrite/executor.py:481-594, 757-793, 852-875).
+ * The MFMA matvec's split-K partials and counters, the LM head's candidate
+ * lists and the MoE layer's plan and activations live in per-device
+ * workspaces shared by every call on that device: such calls must not
+ * overlap (keep them on one stream, or order the streams), and the first
+ * call that grows a workspace must not race with another call.
  *
  * Return codes (pyrite/kernels/native.c:496-525, 562-566):
  *    0  success
