@@ -280,6 +280,32 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     //    padded to chunks of MB.  The order inside a bucket does not matter:
     //    each pair's results are computed independently of its chunk mates.
     const MoePlan& p = a.plan;
+    if (a.batch == 1 && a.MB == 1) {
+        // One token, one pair per chunk: an expert's pair and chunk offsets
+        // are the number of chosen experts below it (the general path's
+        // result, without its buckets and scans; no padding).
+        for (int e = tid; e <= E; e += 256) {
+            int below = 0, hit = 0;
+            for (int j = 0; j < k; ++j) {
+                below += s_top[j] < e;
+                hit += s_top[j] == e;
+            }
+            p.poff[e] = below;
+            p.coff[e] = below;
+            if (e < E) p.cnt[e] = hit;
+        }
+        if (tid < k) {
+            int below = 0;
+            for (int j = 0; j < k; ++j) below += s_top[j] < s_top[tid];
+            p.pair_tok[below] = 0;
+            p.pos[tid] = below;
+        }
+        if (tid == 0) {
+            p.totals[0] = k;
+            p.totals[1] = k;
+        }
+        return;  // a single token never counted an arrival
+    }
     int* s_cnt = s_marked;  // reuse: E ints
     for (int e = tid; e < E; e += 256) s_cnt[e] = 0;
     // every token's ids, read once (device-coherent loads) into LDS
