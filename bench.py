@@ -24,7 +24,8 @@ The line also carries, under "workloads", the other workloads of the
 path, each timed as calls captured in one HIP graph: the single Q4_K
 3072x1024 matvec, the Q6_K 151936x1024 LM head with its exact greedy id, the
 Qwen3-30B-A3B MoE layer (tokens/s at batch 1, 8, 64) and the Llama-3-8B
-Q4_K_M layer (batch-1 decode and 512-token prefill).
+Q4_K_M layer (batch-1 decode and 512-token prefill; its q, gate and down
+matrices also alone at batch 1).
 """
 from __future__ import annotations
 
@@ -366,6 +367,25 @@ def bench_llama(torch, np, quantize, stream, device, lib, sptr):
         res[key] = {"us": round(dt * 1e6, 2), "gbs": round(layer_bytes / dt / 1e9, 1),
                     "pct_hbm_peak": round(100 * layer_bytes / dt / 1e9 / HBM_PEAK_GBS, 2),
                     "tflops": round(flops / dt / 1e12, 2)}
+    del dev
+    # The layer's distinct matrix shapes alone at batch 1, each over rotated
+    # copies of more than 600 MB (beyond the 256 MB Infinity Cache).
+    singles = {}
+    for name, t, rows, cols, p in mats:
+        if name not in ("q", "gate", "down"):
+            continue
+        n = max(2, int(np.ceil(600e6 / p.nbytes)))
+        first = torch.from_numpy(p).cuda()
+        ws1 = [first] + [first.clone() for _ in range(n - 1)]
+        x1 = torch.randn(1, cols, device="cuda")
+        y1 = torch.empty(1, rows, device="cuda")
+        dt = time_graph(torch, stream, [lambda w=w: device.matvec(t, w, x1, rows, cols, out=y1) for w in ws1 * 2])
+        label = {12: "Q4_K", 14: "Q6_K"}[t]
+        singles[f"{name} {rows}x{cols} {label}"] = {
+            "us": round(dt * 1e6, 2), "gbs": round(p.nbytes / dt / 1e9, 1),
+            "pct_hbm_peak": round(100 * p.nbytes / dt / 1e9 / HBM_PEAK_GBS, 2)}
+        del ws1, first
+    res["decode_b1_matrices"] = singles
     return res
 
 
