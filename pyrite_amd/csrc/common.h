@@ -76,27 +76,61 @@ __device__ __forceinline__ void ld_a4x4(const uint8_t* p, uint32_t (&w)[4]) {
     w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
 }
 
+// Global loads at any byte address: gfx950 global loads accept unaligned
+// addresses (the unaligned access mode ROCm runs the GPU in).
+typedef uint32_t u32x4_a1 __attribute__((ext_vector_type(4), aligned(1)));
+typedef uint32_t u32x2_a1 __attribute__((ext_vector_type(2), aligned(1)));
+typedef uint32_t u32_a1 __attribute__((aligned(1)));
+typedef uint16_t u16_a1 __attribute__((aligned(1)));
+
 // N dwords holding bytes [p, p + NB) (NB <= 4N), p of any alignment when !AL.
 // Aligned case: plain dword loads (merged into dwordx4 where possible).
-// Unaligned case: dword-aligned loads whose addresses are clamped to the last
-// dword that still overlaps the span, then v_alignbyte_b32 realigns them; the
-// bytes past NB in the last output word are unspecified.
-template <int NB, bool AL>
+// Unaligned case, UA: dwordx4 / dwordx2 / dword loads at the span's own byte
+// addresses, then a 16- and an 8-bit load for a tail of 1-3 bytes, so every
+// load lies inside the span; the bytes past NB in the last output word are 0.
+// (Fewer instructions; measured faster for the 16-byte spans of the 210- and
+// 110-byte super-blocks, slower for the whole-block spans of the 18- and
+// 34-byte blocks, whose lanes' spans straddle 16-byte boundaries.)
+// Unaligned case, !UA: dword-aligned loads whose addresses are clamped to the
+// last dword that still overlaps the span, then v_alignbyte_b32 realigns them;
+// the bytes past NB in the last output word are unspecified.
+template <int NB, bool AL, bool UA = false>
 __device__ __forceinline__ void ld_span(const uint8_t* p, uint32_t (&w)[(NB + 3) / 4]) {
     constexpr int N = (NB + 3) / 4;
     if constexpr (AL) {
 #pragma unroll
         for (int k = 0; k < N; k += 4) {
-            if constexpr (true) {
-                if (k + 4 <= N) {
-                    uint32_t t[4];
-                    ld_a4x4(p + 4 * k, t);
-                    w[k] = t[0]; w[k + 1] = t[1]; w[k + 2] = t[2]; w[k + 3] = t[3];
-                } else {
+            if (k + 4 <= N) {
+                uint32_t t[4];
+                ld_a4x4(p + 4 * k, t);
+                w[k] = t[0]; w[k + 1] = t[1]; w[k + 2] = t[2]; w[k + 3] = t[3];
+            } else {
 #pragma unroll
-                    for (int j = k; j < N; ++j) w[j] = ld_u32(p + 4 * j);
-                }
+                for (int j = k; j < N; ++j) w[j] = ld_u32(p + 4 * j);
             }
+        }
+    } else if constexpr (UA) {
+        constexpr int K4 = NB / 16 * 4;                     // dwords from dwordx4 loads
+        constexpr int K2 = (NB - 4 * K4) / 8 * 2;           // then from a dwordx2 load
+        constexpr int K1 = (NB - 4 * K4 - 4 * K2) / 4;      // then from a dword load
+        constexpr int REM = NB - 4 * (K4 + K2 + K1);        // tail bytes (0-3)
+#pragma unroll
+        for (int k = 0; k < K4; k += 4) {
+            const u32x4_a1 v = *reinterpret_cast<const u32x4_a1*>(p + 4 * k);
+            w[k] = v.x; w[k + 1] = v.y; w[k + 2] = v.z; w[k + 3] = v.w;
+        }
+        if constexpr (K2 > 0) {
+            const u32x2_a1 v = *reinterpret_cast<const u32x2_a1*>(p + 4 * K4);
+            w[K4] = v.x; w[K4 + 1] = v.y;
+        }
+        if constexpr (K1 > 0) w[K4 + K2] = *reinterpret_cast<const u32_a1*>(p + 4 * (K4 + K2));
+        if constexpr (REM > 0) {
+            constexpr int o = 4 * (K4 + K2 + K1);
+            uint32_t t = 0;
+            if constexpr (REM >= 2) t = *reinterpret_cast<const u16_a1*>(p + o);
+            if constexpr (REM == 3) t |= (uint32_t)p[o + 2] << 16;
+            if constexpr (REM == 1) t = p[o];
+            w[N - 1] = t;
         }
     } else {
         // base = p rounded down to a dword (pointer arithmetic keeps the global

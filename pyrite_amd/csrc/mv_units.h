@@ -199,11 +199,11 @@ template <> struct Unit<T_Q6_K> {
     template <bool AL>
     __device__ __forceinline__ static void load(const uint8_t* blk, int u, Raw& raw) {
         const int h = u >> 1, rr = u & 1;
-        ld_span<16, AL>(blk + 64 * h + 16 * rr, raw.A);
-        ld_span<16, AL>(blk + 64 * h + 32 + 16 * rr, raw.Bq);
-        ld_span<16, AL>(blk + 128 + 32 * h + 16 * rr, raw.H);
-        ld_span<8, AL>(blk + 192 + 8 * h, raw.S);
-        ld_span<2, AL>(blk + 208, raw.D);
+        ld_span<16, AL, true>(blk + 64 * h + 16 * rr, raw.A);
+        ld_span<16, AL, true>(blk + 64 * h + 32 + 16 * rr, raw.Bq);
+        ld_span<16, AL, true>(blk + 128 + 32 * h + 16 * rr, raw.H);
+        ld_span<8, AL, true>(blk + 192 + 8 * h, raw.S);
+        ld_span<2, AL, true>(blk + 208, raw.D);
     }
     template <int B, int R, class XV>
     __device__ __forceinline__ static void dot(const Raw (&raw)[R], int u, const XV& xv,
@@ -327,10 +327,10 @@ template <> struct Unit<T_Q3_K> {
     template <bool AL>
     __device__ __forceinline__ static void load(const uint8_t* blk, int u, Raw& raw) {
         const int h = u >> 1, rr = u & 1;
-        ld_span<16, AL>(blk + 32 + 32 * h + 16 * rr, raw.Q);
-        ld_span<16, AL>(blk + 16 * rr, raw.M);
-        ld_span<12, AL>(blk + 96, raw.S);
-        ld_span<2, AL>(blk + 108, raw.D);
+        ld_span<16, AL, true>(blk + 32 + 32 * h + 16 * rr, raw.Q);
+        ld_span<16, AL, true>(blk + 16 * rr, raw.M);
+        ld_span<12, AL, true>(blk + 96, raw.S);
+        ld_span<2, AL, true>(blk + 108, raw.D);
     }
     template <int B, int R, class XV>
     __device__ __forceinline__ static void dot(const Raw (&raw)[R], int u, const XV& xv,
