@@ -25,7 +25,8 @@ path, each timed as calls captured in one HIP graph: the single Q4_K
 3072x1024 matvec, the Q6_K 151936x1024 LM head with its exact greedy id, the
 Qwen3-30B-A3B MoE layer (tokens/s at batch 1, 8, 64) and the Llama-3-8B
 Q4_K_M layer (batch-1 decode and 512-token prefill; its q, gate and down
-matrices also alone at batch 1).
+matrices also alone at batch 1), and the GGUF -> HBM upload rate of the
+resident-tensor loader.
 """
 from __future__ import annotations
 
@@ -247,6 +248,84 @@ def load_traffic(key: str):
     return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
+def bench_gguf_upload(torch, np):
+    """GGUF file -> HBM: pyrite_amd.resident.ResidentTensors over a 4-layer
+    Llama-3-8B Q4_K_M-shaped checkpoint (551 MB of tensor bytes) written to a
+    temporary file just before, so the file is read from the page cache."""
+    import shutil
+    import struct
+    import tempfile
+
+    from pyrite_amd.gguf import GGUFReader
+    from pyrite_amd.resident import ResidentTensors
+
+    shapes = [("attn_q", 12, 4096, 4096), ("attn_k", 12, 1024, 4096), ("attn_v", 12, 1024, 4096),
+              ("attn_output", 12, 4096, 4096), ("ffn_gate", 12, 14336, 4096), ("ffn_up", 12, 14336, 4096),
+              ("ffn_down", 14, 4096, 14336)]
+    bpb = {12: (256, 144), 14: (256, 210)}
+    tensors = []
+    for layer in range(4):
+        for name, t, rows, cols in shapes:
+            bs, b = bpb[t]
+            tensors.append((f"blk.{layer}.{name}.weight", (cols, rows), t, rows * (cols // bs) * b))
+
+    def s(text):
+        raw = text.encode()
+        return struct.pack("<Q", len(raw)) + raw
+
+    align = 32
+    meta = s("general.alignment") + struct.pack("<II", 4, align)
+    offs, off = [], 0
+    for _, _, _, n in tensors:
+        offs.append(off)
+        off = -(-(off + n) // align) * align
+    head = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), 1) + meta
+    for (name, dims, t, _), o in zip(tensors, offs):
+        head += s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+        head += struct.pack("<IQ", t, o)
+    head += bytes(-len(head) % align)
+    rng = np.random.default_rng(SEED + 40)
+    chunk = rng.integers(0, 256, size=1 << 24, dtype=np.uint8)  # 16 MiB pattern, rotated per tensor
+    tmp = Path(tempfile.mkdtemp(prefix="pyrite_gguf_"))
+    path = tmp / "llama3_8b_4layers.gguf"
+    try:
+        with path.open("wb") as fh:
+            fh.write(head)
+            pos = 0
+            for i, ((_, _, _, n), o) in enumerate(zip(tensors, offs)):
+                fh.write(bytes(o - pos))
+                pattern = np.roll(chunk, 4099 * i)  # a different byte pattern per tensor
+                k = 0
+                while k < n:
+                    m = min(n - k, pattern.size)
+                    fh.write(pattern[:m].tobytes())
+                    k += m
+                pos = o + n
+        total = sum(n for *_, n in tensors)
+        times = []
+        for _ in range(2):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            res = ResidentTensors(GGUFReader(path))
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        # the uploaded bytes are the file's (first MiB of every tensor)
+        reader = GGUFReader(path)
+        for tinfo in reader.tensor_index():
+            with path.open("rb") as fh:
+                fh.seek(tinfo.offset)
+                want = np.frombuffer(fh.read(1 << 20), dtype=np.uint8)
+            if not np.array_equal(res.view(tinfo.name)[:want.size].cpu().numpy(), want):
+                raise RuntimeError(f"uploaded bytes of {tinfo.name} differ from the file")
+        del res
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    best = min(times)
+    return {"workload": "GGUF -> HBM upload (ResidentTensors), 4 Llama-3-8B Q4_K_M layers, page-cached file",
+            "bytes": total, "seconds": round(best, 4), "gbs": round(total / best / 1e9, 2),
+            "first_call_seconds": round(times[0], 4)}
+
+
 def bench_q4k_single(torch, np, quantize, stream, device):
     """Single Q4_K 3072x1024 matvec (Qwen3-0.6B ffn_up), batch 1."""
     rows, cols = 3072, 1024
@@ -399,7 +478,7 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="skip the LM-head, MoE and Llama configurations")
     ap.add_argument("--only", default=None,
                     help="run only the named extra configuration (q4k_3072x1024, lm_head_q6k_151936x1024, "
-                         "moe_qwen3_30b_a3b, llama3_8b_layer, copy_calibration) and print its JSON; "
+                         "moe_qwen3_30b_a3b, llama3_8b_layer, gguf_upload, copy_calibration) and print its JSON; "
                          "for profiling")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -425,6 +504,7 @@ def main() -> int:
                "lm_head_q6k_151936x1024": lambda: bench_lm_head(torch, np, quantize, stream, device),
                "moe_qwen3_30b_a3b": lambda: bench_moe(torch, np, quantize, stream, device),
                "llama3_8b_layer": lambda: bench_llama(torch, np, quantize, stream, device, lib, sptr),
+               "gguf_upload": lambda: bench_gguf_upload(torch, np),
                "copy_calibration": lambda: copy_calibration(torch, stream)}
         print(json.dumps({args.only: fns[args.only]()}), flush=True)
         return 0
@@ -541,7 +621,8 @@ def main() -> int:
                          ("lm_head_q6k_151936x1024", lambda: bench_lm_head(torch, np, quantize, stream, device)),
                          ("moe_qwen3_30b_a3b", lambda: bench_moe(torch, np, quantize, stream, device)),
                          ("llama3_8b_layer", lambda: bench_llama(torch, np, quantize, stream, device, lib,
-                                                                         sptr))):
+                                                                         sptr)),
+                         ("gguf_upload", lambda: bench_gguf_upload(torch, np))):
             log(f"extra configuration: {name}")
             extra[name] = fn()
             torch.cuda.empty_cache()
