@@ -57,6 +57,40 @@ def matvec(type_id: int, w: torch.Tensor, x: torch.Tensor, rows: int, cols: int,
     return out.reshape(rows) if squeeze else out
 
 
+class _MatvecDesc(ctypes.Structure):
+    """pyrite_matvec_desc (include/pyrite_hip.h)."""
+    _fields_ = [("w", ctypes.c_void_p), ("w_len", ctypes.c_size_t), ("rows", ctypes.c_size_t),
+                ("cols", ctypes.c_size_t), ("x", ctypes.c_void_p), ("ldx", ctypes.c_size_t),
+                ("y", ctypes.c_void_p), ("ldy", ctypes.c_size_t)]
+
+
+def matvec_grouped(type_id: int, mats: list[tuple[torch.Tensor, int, int]], x: torch.Tensor,
+                   outs: list[torch.Tensor] | None = None) -> list[torch.Tensor]:
+    """Same-type matrices (w, rows, cols) times the same x in one launch per 16 matrices
+    (a layer's q/k/v or gate/up, pyrite/executor.py:689-697, 672-683).  Each output equals
+    matvec() of that matrix alone, bit for bit."""
+    if not mats:
+        return []
+    squeeze = x.dim() == 1
+    x2 = x.reshape(1, -1) if squeeze else x
+    if x2.dtype != torch.float32 or x2.stride(1) != 1:
+        raise ValueError("x must be fp32 [batch, cols] with contiguous rows")
+    batch = x2.shape[0]
+    if outs is None:
+        outs = [torch.empty(batch, rows, dtype=torch.float32, device=w.device) for w, rows, _ in mats]
+    descs = (_MatvecDesc * len(mats))()
+    for i, ((w, rows, cols), y) in enumerate(zip(mats, outs)):
+        _check_weights(type_id, w, rows, cols)
+        if x2.shape[1] != cols:
+            raise ValueError(f"matrix {i}: x has {x2.shape[1]} columns, the matrix {cols}")
+        y2 = y.reshape(batch, rows)
+        descs[i] = _MatvecDesc(w.data_ptr(), w.numel(), rows, cols, x2.data_ptr(), _ld(x2), y2.data_ptr(), _ld(y2))
+    lib = _lib.load()
+    code = lib.pyrite_dev_matvec_grouped(type_id, descs, len(mats), batch, _stream_ptr(mats[0][0].device))
+    _lib.check(code, "pyrite_dev_matvec_grouped")
+    return [y.reshape(y.shape[-1]) if squeeze else y for y in outs]
+
+
 def dequantize(type_id: int, w: torch.Tensor, rows: int, cols: int,
                dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """Exact dequantization to fp32 or fp64 (fp64 is bit-identical to the reference)."""

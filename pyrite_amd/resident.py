@@ -12,6 +12,8 @@ covers the whole row range):
 
 - ``matrix_matvec``  = ``_matrix_matvec``  (pyrite/executor.py:481-509)
 - ``tensor_matvec``  = ``_tensor_matvec``  (pyrite/executor.py:511-543)
+- ``grouped_matvec`` = the q/k/v and gate/up projections in one launch
+  (pyrite/executor.py:689-697, 672-683)
 - ``expert_slice``   = ``expert_slice``    (pyrite/qwen3_moe.py:364-398)
 - ``slice_matvec``   = ``_slice_matvec``   (pyrite/executor.py:545-594)
 - ``matrix_rows``    = the embedding-row decode (pyrite/executor.py:458-479)
@@ -146,6 +148,21 @@ class ResidentTensors:
         if len(t.dims) != 2 or t.dims != (cols, rows):
             raise ValueError(f"{name} has shape {t.dims}; expected GGML dimensions {(cols, rows)}")
         return self.matrix_matvec(name, 0, rows, x, out=out)
+
+    def grouped_matvec(self, names, x: torch.Tensor) -> list[torch.Tensor]:
+        """Several rank-2 tensors of one type times the same x in one launch (a layer's
+        q/k/v or gate/up, pyrite/executor.py:689-697, 672-683); each result equals
+        tensor_matvec of that tensor, bit for bit."""
+        ts = [self.tensor(n) for n in names]
+        if not ts:
+            return []
+        if any(len(t.dims) != 2 for t in ts):
+            raise ValueError("grouped matvec needs rank-2 tensors")
+        if len({t.ggml_type for t in ts}) != 1:
+            raise ValueError("grouped matvec needs tensors of one GGML type")
+        for t in ts:
+            self._vector(x, t.dims[0], t.name)
+        return _dev.matvec_grouped(ts[0].ggml_type, [(self.view(t.name), t.dims[1], t.dims[0]) for t in ts], x)
 
     def expert_slice(self, name: str, expert: int) -> ExpertSlice:
         """Expert ``expert``'s contiguous slice of a stacked (cols, rows, experts) tensor."""

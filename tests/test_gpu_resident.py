@@ -7,7 +7,7 @@ ResidentTensors.  Checks:
 
 - the HBM arena holds every tensor's file bytes exactly, with a staging buffer
   small enough that tensors straddle chunk boundaries;
-- tensor_matvec / matrix_matvec / slice_matvec over the resident bytes equal
+- tensor_matvec / matrix_matvec / slice_matvec / grouped_matvec over the resident bytes equal
   the device matvec over separately uploaded copies bit for bit, and the
   oracle's fp64 matvec within 1e-4*||x||_2*max|row|;
 - the expert slice's byte range is the oracle's (pyrite/qwen3_moe.py:364-398);
@@ -114,6 +114,25 @@ def test_tensor_and_row_range_matvec(orc, ckpt, res, name, batch):
         part = res.matrix_matvec(name, first, count, xd[0]).cpu().numpy()
         assert np.array_equal(part.view(np.uint32), y[0, first:first + count].view(np.uint32))
         assert res.matrix_matvec(name, rows, 0, xd[0]).numel() == 0
+
+
+@pytest.mark.parametrize("batch", [1, 2, 8])
+def test_grouped_matvec_equals_single_calls(orc, ckpt, res, batch):
+    """The same Q4_K tensor twice in one grouped launch equals the single launch, bit for bit."""
+    _, host = ckpt
+    (cols, rows), _, _ = host["blk.0.attn_q.weight"]
+    announce("resident", "grouped", f"batch={batch}")
+    x = torch.from_numpy(orc.normal(500 + batch, batch * cols).astype(np.float32).reshape(batch, cols)).cuda()
+    names = ["blk.0.attn_q.weight", "blk.0.ffn_gate_exps.weight"]
+    with pytest.raises(ValueError, match="rank-2"):
+        res.grouped_matvec(names, x)
+    with pytest.raises(ValueError, match="one GGML type"):
+        res.grouped_matvec(["blk.0.attn_q.weight", "output.weight"], x)
+    ys = res.grouped_matvec(["blk.0.attn_q.weight", "blk.0.attn_q.weight"], x)
+    single = res.tensor_matvec("blk.0.attn_q.weight", rows, cols, x).cpu().numpy()
+    for y in ys:
+        assert y.shape == (batch, rows)
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), single.view(np.uint32))
 
 
 @pytest.mark.parametrize("comp, rows, cols", [("gate", I, H), ("up", I, H), ("down", H, I)])
