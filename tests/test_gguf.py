@@ -218,3 +218,11 @@ def test_reader_is_lazy_and_checks_missing_files(tmp_path):
     r = GGUFReader(tmp_path / "absent.gguf")  # nothing read yet
     with pytest.raises(FileNotFoundError):
         r.header()
+
+
+def test_resident_tensors_need_a_gpu_device(tmp_path):
+    """The HBM loader refuses a host device before reading anything (no CPU fallback)."""
+    from pyrite_amd.resident import ResidentTensors
+    r = parse(tmp_path, good().bytes())
+    with pytest.raises(ValueError, match="CUDA"):
+        ResidentTensors(r, device="cpu")
