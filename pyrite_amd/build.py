@@ -1,6 +1,7 @@
 """Build libpyrite_hip.so in-tree with hipcc for gfx950.
 
-    python -m pyrite_amd.build          # compile every csrc/*.hip and link
+    python -m pyrite_amd.build          # compile the csrc/*.hip that changed and link
+    python -m pyrite_amd.build --force  # compile every csrc/*.hip
 
 The library lands next to this file (pyrite_amd/libpyrite_hip.so) so that it
 travels with the source tree; objects go to pyrite_amd/_build/.
@@ -39,15 +40,22 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
+def build(verbose: bool = False, jobs: int | None = None, force: bool = False) -> Path:
+    """Compile and link.  Without ``force`` an object is rebuilt only when it is
+    older than its source, any header, or this file (which holds the flags)."""
     BUILD.mkdir(exist_ok=True)
     cc = hipcc()
     srcs = sources()
-    headers = list(CSRC.glob("*.h")) + [HERE.parent / "include" / "pyrite_hip.h"]
+    headers = list(CSRC.glob("*.h")) + [HERE.parent / "include" / "pyrite_hip.h", Path(__file__).resolve()]
     newest_header = max(p.stat().st_mtime for p in headers)
+
+    def stale(src: Path, obj: Path) -> bool:
+        return force or not obj.is_file() or obj.stat().st_mtime < max(src.stat().st_mtime, newest_header)
 
     def compile_one(src: Path) -> Path:
         obj = BUILD / (src.stem + ".o")
+        if not stale(src, obj):
+            return obj
         cmd = [cc, *FLAGS, "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd), flush=True)
@@ -59,7 +67,8 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     n = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)))
     with ThreadPoolExecutor(max_workers=n) as pool:
         objs = list(pool.map(compile_one, srcs))
-    _ = newest_header
+    if not force and LIB.is_file() and all(LIB.stat().st_mtime >= o.stat().st_mtime for o in objs):
+        return LIB
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -70,5 +79,5 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
 
 if __name__ == "__main__":
-    out = build(verbose="-v" in sys.argv)
+    out = build(verbose="-v" in sys.argv, force="--force" in sys.argv)
     print(out)

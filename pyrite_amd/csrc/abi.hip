@@ -11,7 +11,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "pyrite_hip.h"
 #include "dispatch.h"
@@ -74,7 +76,31 @@ struct Staging {
 };
 thread_local Staging g_staging;
 
+std::mutex g_grow_mutex;
+std::vector<void*> g_retired;  // replaced workspace blocks, kept until the process ends
+
 }  // namespace
+
+hipError_t pyrite::workspace_grow(void** block, size_t* cap, size_t want, bool zero, hipStream_t stream) {
+    std::lock_guard<std::mutex> lock(g_grow_mutex);
+    if (*block && *cap >= want) return hipSuccess;  // another caller grew it meanwhile
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+        return hipErrorStreamCaptureUnsupported;
+    size_t bytes = want > 2 * *cap ? want : 2 * *cap;
+    bytes = (bytes + 255) & ~size_t(255);
+    void* fresh = nullptr;
+    hipError_t e = hipMalloc(&fresh, bytes);
+    if (e != hipSuccess) return e;
+    if (zero && (e = hipMemset(fresh, 0, bytes)) != hipSuccess) {
+        (void)hipFree(fresh);
+        return e;
+    }
+    if (*block) g_retired.push_back(*block);
+    *block = fresh;
+    *cap = bytes;
+    return hipSuccess;
+}
 
 extern "C" {
 

@@ -120,6 +120,15 @@ const char* moe_last_error();
 int rms_norm_launch(const float* X, size_t ldx, const float* Wt, size_t n, double eps, float* Y, size_t ldy,
                     size_t batch, hipStream_t stream);
 
+// abi.hip: grow a per-device workspace block to at least `want` bytes
+// (geometrically: at least twice the old capacity), zero-filled when `zero`.
+// The replaced block is never freed: a HIP graph captured before the growth
+// keeps its address, so it stays allocated (and unused by later eager calls)
+// until the process ends; the retired blocks of one workspace add up to less
+// than its live block.  Growth is refused while `stream` is capturing
+// (hipErrorStreamCaptureUnsupported).  Serialised by a process-wide mutex.
+hipError_t workspace_grow(void** block, size_t* cap, size_t want, bool zero, hipStream_t stream);
+
 // dequant.hip: exact dequantization into fp32 (out_f64 == 0) or fp64.
 int dequant_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, void* out, int out_f64,
                    hipStream_t stream);

@@ -263,54 +263,54 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
 // ---------------------------------------------------------------- workspace
 
 struct LmWorkspace {
-    float* bnd = nullptr;
-    size_t bnd_floats = 0;
-    double* L = nullptr;
-    int* cnt = nullptr;
-    int* cand = nullptr;
-    double* candv = nullptr;
-    unsigned int* arrive = nullptr;
-    size_t tokens = 0;
+    void* bnd = nullptr;     // float [tokens][ldl]
+    size_t bnd_cap = 0;      // bytes
+    void* tok = nullptr;     // per token: L, cnt, cand, candv (kLmTokBytes), then arrival counters
+    size_t tok_cap = 0;      // bytes
 };
+
+// Per-token workspace bytes: L (double) and cnt (int) per argmax workgroup,
+// then its candidate rows (int) and their upper bounds (double).
+constexpr size_t kLmTokBytes = (size_t)kLmWgs * (8 + 4 + kLmCand * (4 + 8));
+
+// Carve the token arrays out of one block of `tokens` tokens (arrival counters last).
+static void lm_carve(void* base, size_t tokens, LmArgs& a) {
+    char* p = static_cast<char*>(base);
+    a.ws_L = reinterpret_cast<double*>(p);
+    p += tokens * kLmWgs * sizeof(double);
+    a.ws_candv = reinterpret_cast<double*>(p);
+    p += tokens * kLmWgs * kLmCand * sizeof(double);
+    a.ws_cnt = reinterpret_cast<int*>(p);
+    p += tokens * kLmWgs * sizeof(int);
+    a.ws_cand = reinterpret_cast<int*>(p);
+    p += tokens * kLmWgs * kLmCand * sizeof(int);
+    a.ws_arrive = reinterpret_cast<unsigned int*>(p);
+}
 
 static thread_local const char* g_lm_err = nullptr;
 
-// Per-device workspace, grown on demand (never during stream capture).
+// Per-device workspace, grown on demand (never during stream capture; a
+// replaced block stays allocated for graphs captured before the growth).
+// The token block is zero-filled when allocated, and every launch leaves its
+// arrival counters at zero.
 static int lm_workspace(size_t bnd_floats, size_t tokens, hipStream_t stream, LmWorkspace** out) {
     static LmWorkspace ws[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -4;
     LmWorkspace& w = ws[dev];
-    if (w.bnd_floats >= bnd_floats && w.tokens >= tokens) { *out = &w; return 0; }
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+    const size_t bb = bnd_floats * sizeof(float), tb = tokens * (kLmTokBytes + sizeof(unsigned int));
+    hipError_t e = hipSuccess;
+    if (bb > w.bnd_cap) e = workspace_grow(&w.bnd, &w.bnd_cap, bb, false, stream);
+    if (e == hipSuccess && tb > w.tok_cap) {
+        // the arrival counters sit after the token arrays, whose extent depends
+        // on the capacity in tokens: grow to a whole number of tokens
+        e = workspace_grow(&w.tok, &w.tok_cap, tb, true, stream);
+    }
+    if (e == hipErrorStreamCaptureUnsupported) {
         g_lm_err = "LM-head workspace must grow, which is not allowed during stream capture; run once before capturing";
         return -4;
     }
-    if (hipDeviceSynchronize() != hipSuccess) return -4;
-    if (w.bnd_floats < bnd_floats) {
-        if (w.bnd) (void)hipFree(w.bnd);
-        w.bnd = nullptr;
-        w.bnd_floats = 0;
-        if (hipMalloc(&w.bnd, bnd_floats * sizeof(float)) != hipSuccess) return -4;
-        w.bnd_floats = bnd_floats;
-    }
-    if (w.tokens < tokens) {
-        if (w.L) (void)hipFree(w.L);
-        if (w.cnt) (void)hipFree(w.cnt);
-        if (w.cand) (void)hipFree(w.cand);
-        if (w.candv) (void)hipFree(w.candv);
-        if (w.arrive) (void)hipFree(w.arrive);
-        w.L = nullptr; w.cnt = nullptr; w.cand = nullptr; w.candv = nullptr; w.arrive = nullptr; w.tokens = 0;
-        if (hipMalloc(&w.L, tokens * kLmWgs * sizeof(double)) != hipSuccess) return -4;
-        if (hipMalloc(&w.cnt, tokens * kLmWgs * sizeof(int)) != hipSuccess) return -4;
-        if (hipMalloc(&w.cand, tokens * kLmWgs * kLmCand * sizeof(int)) != hipSuccess) return -4;
-        if (hipMalloc(&w.candv, tokens * kLmWgs * kLmCand * sizeof(double)) != hipSuccess) return -4;
-        if (hipMalloc(&w.arrive, tokens * sizeof(unsigned int)) != hipSuccess) return -4;
-        if (hipMemset(w.arrive, 0, tokens * sizeof(unsigned int)) != hipSuccess) return -4;
-        if (hipDeviceSynchronize() != hipSuccess) return -4;
-        w.tokens = tokens;
-    }
+    if (e != hipSuccess) return -4;
     *out = &w;
     return 0;
 }
@@ -350,7 +350,7 @@ int lm_head_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t
     if (cols > 65536) return -2;
     LmWorkspace* ws = nullptr;
     if (const int rc = lm_workspace(batch * ldl, batch, stream, &ws)) return rc;
-    float* bnd = ws->bnd;
+    float* bnd = static_cast<float*>(ws->bnd);
     if (const int rc = valu_group_launch<true>(type, g, al, &m, &bnd, 1, batch, max_cols, stream, nullptr, nullptr))
         return rc;
     LmArgs a;
@@ -369,11 +369,7 @@ int lm_head_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t
     a.gamma = lm_gamma(g, cols);
     a.abs_margin = 1e-30;
     a.ids = ids;
-    a.ws_L = ws->L;
-    a.ws_cnt = ws->cnt;
-    a.ws_cand = ws->cand;
-    a.ws_candv = ws->candv;
-    a.ws_arrive = ws->arrive;
+    lm_carve(ws->tok, ws->tok_cap / (kLmTokBytes + sizeof(unsigned int)), a);
     if (batch > 65535) return -2;
     hipLaunchKernelGGL(lm_argmax_kernel, dim3(kLmWgs, (unsigned)batch), dim3(256), 0, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -4;

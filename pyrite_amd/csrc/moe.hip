@@ -27,6 +27,7 @@
 //   moe_swiglu_kernel   fit the LDS budget
 //   moe_combine_kernel  out = sum of w * down-out in slot order (fp64 inside)
 #include "dequant.h"
+#include "libm_exp.h"
 #include "mv_kernel.h"
 #include "mx_traits.h"
 
@@ -99,6 +100,18 @@ __device__ double moe_ref_row(int type, const uint8_t* rp, int H, int bs, int bp
     return s;
 }
 
+// The same logit computed by one thread, column after column: a rounded
+// product, then a rounded add, per column.  Used when every row must be exact.
+__device__ double moe_ref_row_seq(int type, const uint8_t* rp, int H, int bs, int bpb, const float* x) {
+    double s = 0.0;
+    for (int c = 0; c < H; ++c) {
+        const int blk = c / bs;
+        s = __dadd_rn(s, __dmul_rn(dq_elem<double>(type, rp + (unsigned long long)blk * bpb, c - blk * bs),
+                                   (double)x[c]));
+    }
+    return s;
+}
+
 // ---------------------------------------------------------------- routing + plan
 
 struct MoePlan {
@@ -149,14 +162,16 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     const float* x = a.X + (unsigned long long)t * a.ldx;
 
     // NaN logits rank last (as -inf), keeping the ranks a total order
+    int nonfinite = 0;
     for (int e = tid; e < E; e += 256) {
         const double l = a.logits[(unsigned long long)t * E + e];
         s_l[e] = isnan(l) ? -INFINITY : l;
         s_b[e] = a.gamma * a.mags[(unsigned long long)t * E + e];
         s_mark[e] = 0;
+        nonfinite |= !isfinite(l) || !isfinite(s_b[e]);
     }
     if (tid == 0) s_nmarked = 0;
-    __syncthreads();
+    nonfinite = __syncthreads_or(nonfinite);
 
     // rank of every expert in (-logit, e) order (a total order: ranks are
     // unique); the first n land in s_top.  Up to 128 experts, two threads
@@ -232,23 +247,83 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
         if (lane == 0) { s_l[e] = isnan(v) ? -INFINITY : v; s_b[e] = 0.0; }
     }
     __syncthreads();
-    if (nm > 0) rank_top(k);
+    if (nm > 0) rank_top(kk);
 
-    // 3. softmax: peak, exp(l - peak) summed (tree order; the reference sums
-    //    left to right, which moves the weights by fp64 rounding only), the
-    //    chosen probabilities, renormalisation and scale
-    // the peak is the first-ranked logit (NaN ranks as -inf, last)
-    const double peak = s_l[s_top[0]];
-    double tot = 0.0;
-    for (int e = tid; e < E; e += 256) tot += exp(s_l[e] - peak);
-    for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off, 64);
-    if (lane == 0) s_red[wave] = tot;
+    // 3. The reference ranks by (-p, e) with p = exp(l - peak) / total
+    //    (pyrite/tensor_ops.py:513-521: exp is the host libm's, total is
+    //    summed left to right), not by (-l, e).  The top k+1 positions above
+    //    are the exact (-l, e) order.  Where each of the first k positions
+    //    leads the next by more than the rounding of l - peak, exp and the
+    //    division can take away (the margin below, for an exp within 1 ulp),
+    //    p strictly decreases along them and every other row has p no larger
+    //    than position k's, so the (-p, e) order of the first k is this one.
+    //    Otherwise (logits within about 2^-48 of each other, or a probability
+    //    near the subnormal range), every row is recomputed exactly and the
+    //    probabilities are formed as the reference forms them.  Non-finite
+    //    logits keep the (-l, e) order, NaN last.
+    __shared__ int s_slow;
+    __shared__ double s_total;
+    if (tid == 0) {
+        int slow = 0;
+        if (!nonfinite) {
+            const double l0 = s_l[s_top[0]], b0 = s_b[s_top[0]];
+            const int np = kk - 1 < k ? kk - 1 : k;  // pairs (i, i + 1), i < k, i + 1 < kk
+            for (int i = 0; i < np; ++i) {
+                const int ea = s_top[i], eb = s_top[i + 1];
+                const double la = s_l[ea], lb = s_l[eb], ba = s_b[ea], bb = s_b[eb];
+                if (ba == 0.0 && bb == 0.0 && la == lb) continue;  // equal exact logits: equal p, index order
+                const double gap = (la - lb) - (ba + bb);
+                const double margin = 0x1p-48 * (1.0 + fabs(la - l0) + fabs(lb - l0) + b0 + ba + bb);
+                if (!(gap > margin) || lb - l0 < -700.0) slow = 1;
+            }
+        }
+        s_slow = slow;
+    }
     __syncthreads();
-    const double total = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+    const bool slow = s_slow;
+    if (slow) {
+        // every row as the reference computes it (pyrite/kernels/native.c:527-553)
+        for (int e = tid; e < E; e += 256) {
+            if (s_b[e] != 0.0) {
+                s_l[e] = moe_ref_row_seq(a.type, a.W + (unsigned long long)e * a.row_bytes, a.H, a.bs, a.bpb, x);
+                s_b[e] = 0.0;
+            }
+        }
+        __syncthreads();
+        // position 0 holds the exact first maximum
+        const double peak = s_l[s_top[0]];
+        for (int e = tid; e < E; e += 256) s_b[e] = libm_exp(s_l[e] - peak);
+        __syncthreads();
+        if (tid == 0) {
+            double tot = 0.0;
+            for (int e = 0; e < E; ++e) tot += s_b[e];
+            s_total = tot;
+        }
+        __syncthreads();
+        // the peak's term is exp(0) = 1, so the total is at least 1
+        for (int e = tid; e < E; e += 256) s_l[e] = s_b[e] / s_total;
+        __syncthreads();
+        rank_top(k);  // by (-p, e) now
+    }
+
+    // 4. the chosen probabilities: exact in the slow case; otherwise each
+    //    exp(l - peak) is the reference's formula and the total a tree sum
+    //    (which moves the weights by fp64 rounding only)
+    const double peak = s_l[s_top[0]];
     __shared__ double s_w[kMoeMaxK];
-    if (tid < k) {
-        const int e = s_top[tid];
-        s_w[tid] = total <= 0.0 ? 1.0 / (double)E : exp(s_l[e] - peak) / total;
+    if (!slow) {
+        double tot = 0.0;
+        for (int e = tid; e < E; e += 256) tot += libm_exp(s_l[e] - peak);
+        for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off, 64);
+        if (lane == 0) s_red[wave] = tot;
+        __syncthreads();
+        const double total = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+        if (tid < k) {
+            const int e = s_top[tid];
+            s_w[tid] = total <= 0.0 ? 1.0 / (double)E : libm_exp(s_l[e] - peak) / total;
+        }
+    } else if (tid < k) {
+        s_w[tid] = s_l[s_top[tid]];
     }
     __syncthreads();
     // slot q's weight: renormalised by the sum of the k probabilities taken
@@ -507,35 +582,29 @@ __global__ __launch_bounds__(kMvThreads) void moe_mv_kernel(const MoeMvArgs a) {
 
 struct MoeWorkspace {
     size_t bytes = 0;
-    char* base = nullptr;
-    unsigned int* arrive = nullptr;
+    void* base = nullptr;
+    void* arrive = nullptr;  // arrival counter (zeroed once; every launch leaves it at zero)
+    size_t arrive_cap = 0;
 };
 
 static thread_local const char* g_moe_err = nullptr;
 const char* moe_last_error() { return g_moe_err; }
 
+// Per-device workspace, grown on demand (never during stream capture; a
+// replaced block stays allocated for graphs captured before the growth).
 static int moe_workspace(size_t bytes, hipStream_t stream, MoeWorkspace** out) {
     static MoeWorkspace ws[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -4;
     MoeWorkspace& w = ws[dev];
-    if (w.bytes >= bytes && w.arrive) { *out = &w; return 0; }
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) {
+    hipError_t e = hipSuccess;
+    if (!w.arrive) e = workspace_grow(&w.arrive, &w.arrive_cap, 256, true, stream);
+    if (e == hipSuccess && w.bytes < bytes) e = workspace_grow(&w.base, &w.bytes, bytes, false, stream);
+    if (e == hipErrorStreamCaptureUnsupported) {
         g_moe_err = "MoE workspace must grow, which is not allowed during stream capture; run once before capturing";
         return -4;
     }
-    if (hipDeviceSynchronize() != hipSuccess) return -4;
-    if (w.base) (void)hipFree(w.base);
-    w.base = nullptr;
-    w.bytes = 0;
-    if (hipMalloc(&w.base, bytes) != hipSuccess) return -4;
-    w.bytes = bytes;
-    if (!w.arrive) {
-        if (hipMalloc(&w.arrive, 256) != hipSuccess) return -4;
-        if (hipMemset(w.arrive, 0, 256) != hipSuccess) return -4;
-    }
-    if (hipDeviceSynchronize() != hipSuccess) return -4;
+    if (e != hipSuccess) return -4;
     *out = &w;
     return 0;
 }
@@ -1046,7 +1115,7 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     layout(c, &logits, &mags, &ids, &wts, &plan, &xg, &g, &u, &act, &yd);
     MoeWorkspace* ws = nullptr;
     if (const int rc = moe_workspace(c.used + 256, stream, &ws)) return rc;
-    Carver cw{ws->base};
+    Carver cw{static_cast<char*>(ws->base)};
     layout(cw, &logits, &mags, &ids, &wts, &plan, &xg, &g, &u, &act, &yd);
 
     // 1. router
@@ -1082,7 +1151,7 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     ra.wts_out = wts_out;
     ra.ids_out = ids_out;
     ra.batch = (int)batch;
-    ra.arrive = ws->arrive;
+    ra.arrive = static_cast<unsigned int*>(ws->arrive);
     ra.plan = plan;
     hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)batch), dim3(256), 0, stream, ra);
     if (hipGetLastError() != hipSuccess) return -4;

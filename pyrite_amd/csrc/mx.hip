@@ -350,14 +350,16 @@ static MxPlanOut mx_plan(MxGroup& grp) {
     return out;
 }
 
-// Split-K workspace, one per device, grown on demand.  Counters are zeroed
-// when allocated and every launch leaves them at zero.  Launches that split K
-// on one device must be ordered on one stream (they share this buffer).
+// Split-K workspace, one per device, grown on demand (never during stream
+// capture; a replaced block stays allocated for graphs captured before).
+// Counters are zeroed when allocated and every launch leaves them at zero.
+// Launches that split K on one device must be ordered on one stream (they
+// share this buffer).
 struct MxWorkspace {
-    float* part = nullptr;
-    size_t part_cap = 0;
-    unsigned* counters = nullptr;
-    size_t counter_cap = 0;
+    void* part = nullptr;
+    size_t part_cap = 0;  // bytes
+    void* counters = nullptr;
+    size_t counter_cap = 0;  // bytes
 };
 static MxWorkspace g_ws[64];
 
@@ -367,31 +369,12 @@ static hipError_t mx_workspace(size_t part_floats, size_t counters, float** part
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess || dev < 0 || dev >= 64) return e != hipSuccess ? e : hipErrorInvalidDevice;
     MxWorkspace& w = g_ws[dev];
-    if (part_floats > w.part_cap || counters > w.counter_cap) {
-        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-        if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
-            return hipErrorStreamCaptureUnsupported;  // grow the workspace before capturing
-        (void)hipStreamSynchronize(stream);
-        if (part_floats > w.part_cap) {
-            if (w.part) (void)hipFree(w.part);
-            w.part = nullptr;
-            w.part_cap = 0;
-            const size_t want = part_floats + part_floats / 2;
-            if ((e = hipMalloc(&w.part, want * sizeof(float))) != hipSuccess) return e;
-            w.part_cap = want;
-        }
-        if (counters > w.counter_cap) {
-            if (w.counters) (void)hipFree(w.counters);
-            w.counters = nullptr;
-            w.counter_cap = 0;
-            const size_t want = counters + counters / 2 + 256;
-            if ((e = hipMalloc(&w.counters, want * sizeof(unsigned))) != hipSuccess) return e;
-            if ((e = hipMemset(w.counters, 0, want * sizeof(unsigned))) != hipSuccess) return e;
-            w.counter_cap = want;
-        }
-    }
-    *part = w.part;
-    *ctr = w.counters;
+    const size_t pb = part_floats * sizeof(float), cb = (counters + 256) * sizeof(unsigned);
+    if (pb > w.part_cap && (e = workspace_grow(&w.part, &w.part_cap, pb, false, stream)) != hipSuccess) return e;
+    if (cb > w.counter_cap && (e = workspace_grow(&w.counters, &w.counter_cap, cb, true, stream)) != hipSuccess)
+        return e;
+    *part = static_cast<float*>(w.part);
+    *ctr = static_cast<unsigned*>(w.counters);
     return hipSuccess;
 }
 

@@ -39,20 +39,51 @@ def _check_weights(type_id: int, w: torch.Tensor, rows: int, cols: int) -> None:
         raise ValueError(f"{t.name} needs cols divisible by {t.block_size}")
 
 
+def _activations(x: torch.Tensor, device: torch.device, cols: int, name: str = "x") -> torch.Tensor:
+    """x as a [batch, cols] view: fp32, on ``device``, rows contiguous.
+
+    The kernels dereference the pointer on the GPU, so a host tensor or a
+    tensor on another device is refused here, before any launch."""
+    if not isinstance(x, torch.Tensor) or not x.is_cuda or x.device != device:
+        raise ValueError(f"{name} must be a CUDA tensor on {device}")
+    x2 = x.reshape(1, -1) if x.dim() == 1 else x
+    if x2.dim() != 2 or x2.dtype != torch.float32 or x2.shape[1] != cols or x2.stride(1) != 1:
+        raise ValueError(f"{name} must be fp32 [batch, {cols}] with contiguous rows")
+    if x2.shape[0] < 1:
+        raise ValueError(f"{name} has no vectors")
+    return x2
+
+
+def _output(y: torch.Tensor, device: torch.device, batch: int, n: int, name: str = "out") -> torch.Tensor:
+    """An output as a [batch, n] view of the caller's own memory (never a copy).
+
+    1-D outputs are accepted for batch 1.  Rows must be contiguous and must
+    not overlap (stride(0) >= n), so every kernel write lands in ``y``."""
+    if not isinstance(y, torch.Tensor) or not y.is_cuda or y.device != device:
+        raise ValueError(f"{name} must be a CUDA tensor on {device}")
+    if y.dtype != torch.float32:
+        raise ValueError(f"{name} must be fp32")
+    if y.dim() == 1 and batch == 1 and y.shape[0] == n and (n == 1 or y.stride(0) == 1):
+        return y.view(1, n)
+    if (y.dim() == 2 and tuple(y.shape) == (batch, n) and (n == 1 or y.stride(1) == 1)
+            and (batch == 1 or y.stride(0) >= n)):
+        return y
+    raise ValueError(f"{name} must be fp32 [{batch}, {n}] (or [{n}] for one vector) with contiguous rows")
+
+
 def matvec(type_id: int, w: torch.Tensor, x: torch.Tensor, rows: int, cols: int,
            out: torch.Tensor | None = None) -> torch.Tensor:
     """y[b] = dequant(w) @ x[b]; x is [cols] or [batch, cols] fp32 (last dim contiguous)."""
     _check_weights(type_id, w, rows, cols)
     squeeze = x.dim() == 1
-    x2 = x.reshape(1, -1) if squeeze else x
-    if x2.dtype != torch.float32 or x2.shape[1] != cols or x2.stride(1) != 1:
-        raise ValueError("x must be fp32 [batch, cols] with contiguous rows")
+    x2 = _activations(x, w.device, cols)
     batch = x2.shape[0]
     if out is None:
         out = torch.empty(batch, rows, dtype=torch.float32, device=w.device)
+    y2 = _output(out, w.device, batch, rows)
     lib = _lib.load()
     code = lib.pyrite_dev_matvec(type_id, w.data_ptr(), w.numel(), rows, cols, x2.data_ptr(), _ld(x2),
-                                 out.data_ptr(), _ld(out), batch, _stream_ptr(w.device))
+                                 y2.data_ptr(), _ld(y2), batch, _stream_ptr(w.device))
     _lib.check(code, "pyrite_dev_matvec")
     return out.reshape(rows) if squeeze else out
 
@@ -72,18 +103,21 @@ def matvec_grouped(type_id: int, mats: list[tuple[torch.Tensor, int, int]], x: t
     if not mats:
         return []
     squeeze = x.dim() == 1
-    x2 = x.reshape(1, -1) if squeeze else x
-    if x2.dtype != torch.float32 or x2.stride(1) != 1:
-        raise ValueError("x must be fp32 [batch, cols] with contiguous rows")
+    dev = mats[0][0].device
+    x2 = _activations(x, dev, x.shape[-1])
     batch = x2.shape[0]
     if outs is None:
         outs = [torch.empty(batch, rows, dtype=torch.float32, device=w.device) for w, rows, _ in mats]
+    if len(outs) != len(mats):
+        raise ValueError(f"{len(mats)} matrices but {len(outs)} outputs")
     descs = (_MatvecDesc * len(mats))()
     for i, ((w, rows, cols), y) in enumerate(zip(mats, outs)):
         _check_weights(type_id, w, rows, cols)
+        if w.device != dev:
+            raise ValueError(f"matrix {i} is on {w.device}, matrix 0 on {dev}")
         if x2.shape[1] != cols:
             raise ValueError(f"matrix {i}: x has {x2.shape[1]} columns, the matrix {cols}")
-        y2 = y.reshape(batch, rows)
+        y2 = _output(y, dev, batch, rows, f"outs[{i}]")
         descs[i] = _MatvecDesc(w.data_ptr(), w.numel(), rows, cols, x2.data_ptr(), _ld(x2), y2.data_ptr(), _ld(y2))
     lib = _lib.load()
     code = lib.pyrite_dev_matvec_grouped(type_id, descs, len(mats), batch, _stream_ptr(mats[0][0].device))
@@ -114,16 +148,15 @@ def lm_head_argmax(type_id: int, w: torch.Tensor, x: torch.Tensor, rows: int, co
     reference's fp64 logits (pyrite/executor.py:852-875, pyrite/sampler.py:12-15).
     """
     _check_weights(type_id, w, rows, cols)
-    x2 = x.reshape(1, -1) if x.dim() == 1 else x
-    if x2.dtype != torch.float32 or x2.shape[1] != cols or x2.stride(1) != 1:
-        raise ValueError("x must be fp32 [batch, cols] with contiguous rows")
+    x2 = _activations(x, w.device, cols)
     batch = x2.shape[0]
     if logits is None:
         logits = torch.empty(batch, rows, dtype=torch.float32, device=w.device)
+    l2 = _output(logits, w.device, batch, rows, "logits")
     ids = torch.empty(batch, dtype=torch.int32, device=w.device)
     lib = _lib.load()
     code = lib.pyrite_dev_lm_head_argmax(type_id, w.data_ptr(), w.numel(), rows, cols, x2.data_ptr(),
-                                         _ld(x2), logits.data_ptr(), _ld(logits), ids.data_ptr(),
+                                         _ld(x2), l2.data_ptr(), _ld(l2), ids.data_ptr(),
                                          batch, _stream_ptr(w.device))
     _lib.check(code, "pyrite_dev_lm_head_argmax")
     return logits, ids
@@ -131,12 +164,13 @@ def lm_head_argmax(type_id: int, w: torch.Tensor, x: torch.Tensor, rows: int, co
 
 def rms_norm(x: torch.Tensor, weight: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
     """RMSNorm over the last dim of fp32 x (pyrite/tensor_ops.py:502-506), fp64 inside."""
-    x2 = x.reshape(1, -1) if x.dim() == 1 else x
-    if x2.dtype != torch.float32 or not x2.is_cuda or x2.stride(1) != 1:
+    if not isinstance(x, torch.Tensor) or not x.is_cuda:
         raise ValueError("x must be an fp32 CUDA tensor with contiguous rows")
+    x2 = _activations(x, x.device, x.shape[-1])
     n = x2.shape[1]
-    if weight is not None and (weight.dtype != torch.float32 or weight.numel() != n or not weight.is_contiguous()):
-        raise ValueError("weight must be a contiguous fp32 tensor of x's last dim")
+    if weight is not None and (weight.dtype != torch.float32 or weight.numel() != n or not weight.is_contiguous()
+                               or weight.device != x2.device):
+        raise ValueError("weight must be a contiguous fp32 tensor of x's last dim on x's device")
     y = torch.empty_like(x2)
     lib = _lib.load()
     code = lib.pyrite_dev_rms_norm(x2.data_ptr(), _ld(x2), weight.data_ptr() if weight is not None else None,
@@ -183,6 +217,8 @@ class MoeLayer:
         for t in (self.router, self.gate, self.up, self.down):
             if t.dtype != torch.uint8 or not t.is_cuda or not t.is_contiguous():
                 raise ValueError("MoE tensors must be contiguous uint8 CUDA tensors")
+            if t.device != self.router.device:
+                raise ValueError("MoE tensors must be on one device")
         return _MoeLayerC(self.router_type, self.router.data_ptr(), self.router.numel(),
                           self.gate_type, self.gate.data_ptr(), self.gate.numel(),
                           self.up_type, self.up.data_ptr(), self.up.numel(),
@@ -198,17 +234,17 @@ def moe_ffn(layer: MoeLayer, x: torch.Tensor, out: torch.Tensor | None = None
     Returns (out [batch, hidden] fp32, ids [batch, k] int32 in rank order,
     weights [batch, k] fp32); the ids equal the reference's expert choice.
     """
-    x2 = x.reshape(1, -1) if x.dim() == 1 else x
-    if x2.dtype != torch.float32 or x2.shape[1] != layer.hidden or x2.stride(1) != 1 or not x2.is_cuda:
-        raise ValueError("x must be an fp32 CUDA tensor [batch, hidden] with contiguous rows")
+    dev = layer.router.device
+    x2 = _activations(x, dev, layer.hidden)
     batch = x2.shape[0]
     if out is None:
-        out = torch.empty(batch, layer.hidden, dtype=torch.float32, device=x2.device)
-    ids = torch.empty(batch, layer.k, dtype=torch.int32, device=x2.device)
-    wts = torch.empty(batch, layer.k, dtype=torch.float32, device=x2.device)
+        out = torch.empty(batch, layer.hidden, dtype=torch.float32, device=dev)
+    o2 = _output(out, dev, batch, layer.hidden)
+    ids = torch.empty(batch, layer.k, dtype=torch.int32, device=dev)
+    wts = torch.empty(batch, layer.k, dtype=torch.float32, device=dev)
     c = layer._c()
     lib = _lib.load()
-    code = lib.pyrite_dev_moe_ffn(ctypes.addressof(c), x2.data_ptr(), _ld(x2), out.data_ptr(), _ld(out),
-                                  ids.data_ptr(), wts.data_ptr(), batch, _stream_ptr(x2.device))
+    code = lib.pyrite_dev_moe_ffn(ctypes.addressof(c), x2.data_ptr(), _ld(x2), o2.data_ptr(), _ld(o2),
+                                  ids.data_ptr(), wts.data_ptr(), batch, _stream_ptr(dev))
     _lib.check(code, "pyrite_dev_moe_ffn")
     return out, ids, wts

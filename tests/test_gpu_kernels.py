@@ -376,3 +376,40 @@ def test_device_matvec_nonfinite_activations(torch_dev, t, batch):
             err = np.abs(y[b][fin].astype(np.float64) - ref[fin])
             xf = np.where(np.isfinite(xs[b]), xs[b], 0.0)
             assert np.all(err <= 1e-4 * np.linalg.norm(xf) * rowmax[fin]), f"b{b}: finite rows off"
+
+
+# The 512-token prefill of one Llama-3-8B layer in the Q4_K_M mix (the MFMA
+# dequant-GEMM: 16 token tiles of 32).  Tokens checked against the oracle:
+# every token of the first and the last token tile and every 8th token between.
+LLAMA_LAYER = [("q", 12, 4096, 4096), ("k", 12, 1024, 4096), ("v", 12, 1024, 4096), ("o", 12, 4096, 4096),
+               ("gate", 12, 14336, 4096), ("up", 12, 14336, 4096), ("down", 14, 4096, 14336)]
+PREFILL_TOKENS = sorted(set(range(32)) | set(range(480, 512)) | set(range(0, 512, 8)))
+_PREFILL_PAYLOADS: dict = {}
+
+
+@pytest.mark.parametrize("name,t,rows,cols", LLAMA_LAYER, ids=[m[0] for m in LLAMA_LAYER])
+def test_llama_layer_prefill_512(torch_dev, name, t, rows, cols):
+    from concurrent.futures import ThreadPoolExecutor
+
+    from pyrite_amd import device
+
+    torch = torch_dev
+    o = oracle()
+    seed = 20245500 + rows + cols
+    if (t, rows, cols) not in _PREFILL_PAYLOADS:  # q/o, k/v and gate/up share their weights
+        _PREFILL_PAYLOADS[(t, rows, cols)] = o.quantize(t, o.normal(seed, rows * cols, 0.0, 0.02).astype(np.float64))
+    payload = _PREFILL_PAYLOADS[(t, rows, cols)]
+    xs = np.stack([o.normal(seed + 1 + b, cols) for b in range(512)]).astype(np.float32)
+    announce("llama_prefill_512", name, TYPES[t][0], rows, cols, 512)
+    y = device.matvec(t, device.upload(payload.tobytes()), torch.from_numpy(xs).cuda(), rows, cols).cpu().numpy()
+    rb = row_bytes(t, cols)
+    rowmax = np.concatenate([
+        np.abs(o.dequantize_rows(t, payload[r0 * rb:min(rows, r0 + 1024) * rb], min(1024, rows - r0), cols)
+               .reshape(-1, cols)).max(axis=1) for r0 in range(0, rows, 1024)])
+
+    def ref(b):  # the oracle call releases the GIL
+        return b, o.matvec(t, payload, xs[b].astype(np.float64), rows, cols)
+
+    with ThreadPoolExecutor(8) as pool:
+        for b, r in pool.map(ref, PREFILL_TOKENS):
+            assert_matvec_close(y[b], r, xs[b], rowmax, f"prefill {name} {rows}x{cols} token {b}/512")

@@ -167,3 +167,126 @@ def test_moe_qwen3_30b_shape(orc, dev):
     for batch in (1, 8, 64):
         xs = np.stack([orc.normal(20244100 + b, 2048) for b in range(batch)])
         _check(orc, layer, host, xs, f"qwen3-30b b={batch}")
+
+
+# ---------------------------------------------------------------- (-p, e) ranking
+# The reference ranks experts by (-p, e), p = exp(l - peak) / total
+# (pyrite/executor.py:765-767, pyrite/tensor_ops.py:513-521).  Distinct fp64
+# logits can give equal probabilities (l - peak rounds them together, exp
+# rounds them together, or the division does), and the lower index then ranks
+# first even though its logit is smaller.  These routers are F64 with rows
+# whose only nonzero weight is in column 0 and x[0] = 1, so those rows' logits
+# are exactly their weights; every other row is dense, so its exact logit
+# (which enters the total) needs the reference's own summation order.
+
+def _tie_layer(orc, E, H, crafted, seed):
+    from pyrite_amd import device
+    rng = np.random.default_rng(seed)
+    w = rng.normal(0.0, 0.002, size=(E, H))
+    for e, v in crafted.items():
+        w[e] = 0.0
+        w[e, 0] = v
+    router = np.ascontiguousarray(w, dtype=np.float64).view(np.uint8).reshape(-1).copy()
+    I = 256
+    gate = _fast_random(rng, 12, E * I, H)
+    up = _fast_random(rng, 12, E * I, H)
+    down = _fast_random(rng, 14, E * H, I)
+    d = torch.device("cuda:0")
+    layer = device.MoeLayer(28, torch.from_numpy(router).to(d), 12, torch.from_numpy(gate).to(d),
+                            12, torch.from_numpy(up).to(d), 14, torch.from_numpy(down).to(d), E, H, I, 8)
+    return layer, (router, gate, up, down)
+
+
+def _tie_x(orc, H, seed):
+    x = orc.normal(seed, H).astype(np.float32)
+    x[0] = 1.0
+    return x
+
+
+def _ref_route(orc, router, E, H, x, k=8):
+    logits = orc.matvec(28, router, x.astype(np.float64), E, H)
+    ids, w, probs = orc.route(logits, k)
+    by_logit = sorted(range(E), key=lambda e: (-logits[e], e))[:k]
+    return logits, list(ids), probs, by_logit
+
+
+def test_moe_rank_tie_at_peak(orc, dev):
+    """Logits 0.3 (expert 40) and the next double below (expert 7): the
+    probabilities are equal, so expert 7 ranks first."""
+    E, H = 128, 256
+    v = 0.3
+    layer, host = _tie_layer(orc, E, H, {40: v, 7: float(np.nextafter(v, 0.0))}, seed=5101)
+    x = _tie_x(orc, H, 5102)
+    logits, ids, probs, by_logit = _ref_route(orc, host[0], E, H, x)
+    assert ids[:2] == [7, 40] and by_logit[:2] == [40, 7] and probs[7] == probs[40], "case does not tie"
+    _check(orc, layer, host, x[None, :], "tie at the peak")
+
+
+def test_moe_rank_tie_at_boundary(orc, dev):
+    """Two logits one double apart at the k-th place: the lower index (20)
+    takes the last slot although expert 50's logit is larger."""
+    E, H = 128, 256
+    crafted = {3: 1.0, 10: 0.9, 11: 0.85, 12: 0.8, 13: 0.75, 14: 0.7, 15: 0.65}
+    # 0.2 + j * 2^-55 and the double below it differ by a quarter ulp of
+    # their difference from the peak, so l - peak often rounds them together;
+    # the dense rows stay far below, so the crafted logits alone decide
+    for j in range(1, 4000):
+        c = 0.2 + j * 2.0 ** -55
+        cr = {**crafted, 50: c, 20: float(np.nextafter(c, 0.0))}
+        lg = np.array([cr.get(e, -1.0) for e in range(E)])
+        ids, _, p = orc.route(lg, 8)
+        if 20 in ids and 50 not in ids:
+            break
+    else:
+        pytest.fail("no boundary tie found")
+    layer, host = _tie_layer(orc, E, H, cr, seed=5201)
+    x = _tie_x(orc, H, 5202)
+    logits, ids, probs, by_logit = _ref_route(orc, host[0], E, H, x)
+    assert 20 in ids and 50 not in ids and 50 in by_logit and 20 not in by_logit, "case does not tie"
+    _check(orc, layer, host, x[None, :], "tie at the boundary")
+
+
+def test_moe_rank_tie_in_division(orc, dev):
+    """exp(l - peak) differs by one ulp between experts 9 and 60, yet
+    dividing by the total rounds both probabilities to one value: expert 9
+    (the smaller exp) ranks first.  Needs the exact total, i.e. every row's
+    exact logit and the left-to-right sum."""
+    import math
+    E, H = 128, 256
+    x = _tie_x(orc, H, 5302)
+    found = None
+    # exp values just below 1 (the top of their binade) and probabilities
+    # near the bottom of theirs: a one-ulp step in exp is then often less
+    # than one ulp of the quotient
+    base = np.random.default_rng(5301).normal(0.0, 0.002, size=(E, H))
+    for j in range(1, 200):
+        va = 1.0 - j * 2.0 ** -20
+        for d in range(1, 4):
+            vb = va - d * 2.0 ** -53
+            cr = {0: 1.0, 33: 0.95, 60: va, 9: vb}
+            w = base.copy()
+            for e, val in cr.items():
+                w[e] = 0.0
+                w[e, 0] = val
+            router = np.ascontiguousarray(w).view(np.uint8).reshape(-1)
+            logits, ids, probs, by_logit = _ref_route(orc, router, E, H, x)
+            peak = max(logits)
+            ea, eb = math.exp(logits[60] - peak), math.exp(logits[9] - peak)
+            if ea != eb and probs[60] == probs[9] and ids.index(9) < ids.index(60):
+                found = cr
+                break
+        if found:
+            break
+    assert found, "no division tie found"
+    layer, host = _tie_layer(orc, E, H, found, seed=5301)
+    _check(orc, layer, host, x[None, :], "tie in the division")
+
+
+def test_moe_rank_ties_batch(orc, dev):
+    """The peak tie as the first and last token of a batch, ordinary tokens
+    between them: each token takes its own path through the ranking."""
+    E, H = 128, 256
+    v = 0.3
+    layer, host = _tie_layer(orc, E, H, {40: v, 7: float(np.nextafter(v, 0.0))}, seed=5101)
+    xs = np.stack([_tie_x(orc, H, 5102)] + [orc.normal(5400 + b, H) for b in range(5)] + [_tie_x(orc, H, 5102)])
+    _check(orc, layer, host, xs.astype(np.float32), "ties in a batch")
