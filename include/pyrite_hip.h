@@ -116,6 +116,19 @@ int pyrite_dev_lm_head_argmax(int type_id, const void *w, size_t w_len, size_t r
                               const float *x, size_t ldx, float *logits, size_t ldl, int32_t *ids,
                               size_t batch, void *stream);
 
+/* pyrite_dev_lm_head_argmax without any allocation, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  Same
+ * arguments, results and codes as pyrite_dev_lm_head_argmax; its workspace is
+ * a fixed 8 MiB device array in the library (one per GPU, kept until the
+ * process ends) instead of memory allocated on first use.  Limits: batch <= 8
+ * and (batch - 1) * ldl + rows <= 1894336 (e.g. 8 vectors of a 151936-row
+ * vocabulary), else -2.  Every call on one GPU shares the array: calls that
+ * overlap on one GPU (different streams, or host threads) race. */
+int pyrite_dev_lm_head_argmax_noalloc(int type_id, const void *w, size_t w_len, size_t rows, size_t cols,
+                                      const float *x, size_t ldx, float *logits, size_t ldl, int32_t *ids,
+                                      size_t batch, void *stream);
+
 /* One Qwen3-MoE FFN layer.  Tensors are GGUF bytes in device memory: the
  * router [n_experts][hidden] (ffn_gate_inp), and the stacked expert tensors
  * gate and up [n_experts][inter][hidden] and down [n_experts][hidden][inter]

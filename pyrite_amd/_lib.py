@@ -27,6 +27,8 @@ SIGNATURES: list[tuple[str, object, tuple]] = [
     ("pyrite_dev_matvec_grouped_timed", _c.c_int, (_c.c_int, _vp, _sz, _sz, _vp, _vp, _vp)),
     ("pyrite_dev_dequantize", _c.c_int, (_c.c_int, _vp, _sz, _sz, _sz, _vp, _c.c_int, _vp)),
     ("pyrite_dev_lm_head_argmax", _c.c_int, (_c.c_int, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp)),
+    ("pyrite_dev_lm_head_argmax_noalloc", _c.c_int,
+     (_c.c_int, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp)),
     ("pyrite_dev_moe_ffn", _c.c_int, (_vp, _vp, _sz, _vp, _sz, _vp, _vp, _sz, _vp)),
     ("pyrite_dev_rms_norm", _c.c_int, (_vp, _sz, _vp, _sz, _c.c_double, _vp, _sz, _sz, _vp)),
 ]

@@ -211,6 +211,19 @@ int pyrite_dev_lm_head_argmax(int type_id, const void* w, size_t w_len, size_t r
     return rc;
 }
 
+int pyrite_dev_lm_head_argmax_noalloc(int type_id, const void* w, size_t w_len, size_t rows, size_t cols,
+                                      const float* x, size_t ldx, float* logits, size_t ldl, int32_t* ids,
+                                      size_t batch, void* stream) {
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;
+    const int rc = lm_head_noalloc_launch(type_id, static_cast<const uint8_t*>(w), w_len, rows, cols, x, ldx,
+                                          logits, ldl, reinterpret_cast<int*>(ids), batch, s);
+    if (rc != 0) {
+        if (const char* m = lm_last_error()) return fail(rc, m);
+        if (rc == -4) return fail(-4, "pyrite_dev_lm_head_argmax_noalloc: launch", hipGetLastError());
+    }
+    return rc;
+}
+
 int pyrite_dev_moe_ffn(const pyrite_moe_layer* layer, const float* x, size_t ldx, float* out, size_t ldo,
                        int32_t* ids, float* weights, size_t batch, void* stream) {
     static_assert(sizeof(pyrite_moe_layer) == sizeof(MoeLayer), "MoE layer layout");

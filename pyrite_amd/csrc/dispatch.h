@@ -88,6 +88,10 @@ int matvec64_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_
 // maximum of the reference's fp64 logits, for b < batch.
 int lm_head_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* X, size_t ldx,
                    float* logits, size_t ldl, int* ids, size_t batch, hipStream_t stream);
+// The same over a fixed device scratch array (no allocation): batch <= 8 and
+// (batch - 1) * ldl + rows <= 1894336.
+int lm_head_noalloc_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* X,
+                           size_t ldx, float* logits, size_t ldl, int* ids, size_t batch, hipStream_t stream);
 const char* lm_last_error();
 
 // moe.hip: one Qwen3-MoE FFN layer (router, top-k, experts, combine) for

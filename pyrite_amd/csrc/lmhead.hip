@@ -25,6 +25,8 @@
 // The argmax kernel runs NWG workgroups per token; each reduces a row range
 // and lists its local candidates, and the last to finish (arrival counter,
 // reset by that workgroup) decides.
+#include <mutex>
+
 #include "dequant.h"
 #include "mv_kernel.h"
 
@@ -338,41 +340,126 @@ static double lm_gamma(const TypeGeo& g, size_t cols) {
     return (g32 + g64) * (1 + 1.0 / 1024);
 }
 
-int lm_head_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* X, size_t ldx,
-                   float* logits, size_t ldl, int* ids, size_t batch, hipStream_t stream) {
-    g_lm_err = nullptr;
-    const TypeGeo g = type_geo(type);
-    MatvecArgs m{W, w_len, rows, cols, X, ldx, logits, ldl};
-    bool al = false;
-    size_t max_cols = 0;
-    if (const int rc = validate_group(g, &m, 1, batch, &al, &max_cols)) return rc;
-    if (!ids) return -3;
-    if (cols > 65536) return -2;
-    LmWorkspace* ws = nullptr;
-    if (const int rc = lm_workspace(batch * ldl, batch, stream, &ws)) return rc;
-    float* bnd = static_cast<float*>(ws->bnd);
+// Zero the arrival counters of `n` tokens (a kernel, not a memset, so that it
+// can be captured into a graph).
+__global__ __launch_bounds__(256) void lm_clear_kernel(unsigned int* counters, int n) {
+    for (int i = threadIdx.x; i < n; i += 256) counters[i] = 0u;
+}
+
+// The bound matvec, then the argmax kernel, over workspace memory the caller
+// provides: bnd (floats laid out like the logits) and a token block carved by
+// lm_carve for `tok_cap` tokens.  clear: zero the arrival counters first.
+static int lm_head_run(int type, const TypeGeo& g, bool al, size_t max_cols, const MatvecArgs& m, int* ids,
+                       size_t batch, float* bnd, void* tok, size_t tok_cap, bool clear, hipStream_t stream) {
+    LmArgs a;
+    lm_carve(tok, tok_cap, a);
+    if (clear) {
+        hipLaunchKernelGGL(lm_clear_kernel, dim3(1), dim3(256), 0, stream, a.ws_arrive, (int)batch);
+        if (hipGetLastError() != hipSuccess) return -4;
+    }
     if (const int rc = valu_group_launch<true>(type, g, al, &m, &bnd, 1, batch, max_cols, stream, nullptr, nullptr))
         return rc;
-    LmArgs a;
     a.type = type;
     a.bs = g.bs;
     a.bpb = g.bpb;
-    a.W = W;
-    a.row_bytes = cols / g.bs * g.bpb;
-    a.rows = (int)rows;
-    a.cols = (int)cols;
-    a.X = X;
-    a.ldx = ldx;
-    a.Y = logits;
+    a.W = static_cast<const uint8_t*>(m.w);
+    a.row_bytes = m.cols / g.bs * g.bpb;
+    a.rows = (int)m.rows;
+    a.cols = (int)m.cols;
+    a.X = m.x;
+    a.ldx = m.ldx;
+    a.Y = m.y;
     a.Bnd = bnd;
-    a.ldy = ldl;
-    a.gamma = lm_gamma(g, cols);
+    a.ldy = m.ldy;
+    a.gamma = lm_gamma(g, m.cols);
     a.abs_margin = 1e-30;
     a.ids = ids;
-    lm_carve(ws->tok, ws->tok_cap / (kLmTokBytes + sizeof(unsigned int)), a);
-    if (batch > 65535) return -2;
     hipLaunchKernelGGL(lm_argmax_kernel, dim3(kLmWgs, (unsigned)batch), dim3(256), 0, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+static int lm_validate(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* X,
+                       size_t ldx, float* logits, size_t ldl, int* ids, size_t batch, TypeGeo* g, MatvecArgs* m,
+                       bool* al, size_t* max_cols) {
+    *g = type_geo(type);
+    *m = MatvecArgs{W, w_len, rows, cols, X, ldx, logits, ldl};
+    if (const int rc = validate_group(*g, m, 1, batch, al, max_cols)) return rc;
+    if (!ids) return -3;
+    if (cols > 65536 || batch > 65535) return -2;
+    return 0;
+}
+
+int lm_head_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* X, size_t ldx,
+                   float* logits, size_t ldl, int* ids, size_t batch, hipStream_t stream) {
+    g_lm_err = nullptr;
+    TypeGeo g;
+    MatvecArgs m;
+    bool al = false;
+    size_t max_cols = 0;
+    if (const int rc = lm_validate(type, W, w_len, rows, cols, X, ldx, logits, ldl, ids, batch, &g, &m, &al,
+                                   &max_cols))
+        return rc;
+    LmWorkspace* ws = nullptr;
+    if (const int rc = lm_workspace(batch * ldl, batch, stream, &ws)) return rc;
+    return lm_head_run(type, g, al, max_cols, m, ids, batch, static_cast<float*>(ws->bnd), ws->tok,
+                       ws->tok_cap / (kLmTokBytes + sizeof(unsigned int)), false, stream);
+}
+
+// ---------------------------------------------------------------- allocation-free variant
+// The LM head for callers that cannot allocate (code under graph capture,
+// serving loops): its workspace is this file-scope device array instead of
+// hipMalloc'ed memory.  Layout: the token block for kLmScratchTokens tokens
+// (lm_carve), then, from the next 256-byte boundary, the bound floats.  Each
+// GPU holds its own copy until the process ends; every call on a GPU shares it
+// (the last call's contents stay), so calls that overlap on one GPU race.
+constexpr size_t kLmScratchBytes = size_t(8) << 20;
+constexpr size_t kLmScratchTokens = 8;
+constexpr size_t kLmScratchBndOffset =
+    (kLmScratchTokens * (kLmTokBytes + sizeof(unsigned int)) + 255) & ~size_t(255);
+constexpr size_t kLmScratchBndFloats = (kLmScratchBytes - kLmScratchBndOffset) / sizeof(float);
+static_assert(kLmScratchBndFloats == 1894336, "the limit quoted in the error message and the header");
+
+static __device__ __align__(256) unsigned char scratch[kLmScratchBytes];
+
+// The device address of `scratch` on the current device (its host-side name
+// is only a stand-in), looked up once per device.
+static int lm_scratch(void** out) {
+    static std::mutex mu;
+    static void* ptr[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -4;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+            g_lm_err = "hipGetSymbolAddress of the LM-head scratch failed";
+            return -4;
+        }
+        ptr[dev] = p;
+    }
+    *out = ptr[dev];
+    return 0;
+}
+
+int lm_head_noalloc_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* X,
+                           size_t ldx, float* logits, size_t ldl, int* ids, size_t batch, hipStream_t stream) {
+    g_lm_err = nullptr;
+    TypeGeo g;
+    MatvecArgs m;
+    bool al = false;
+    size_t max_cols = 0;
+    if (const int rc = lm_validate(type, W, w_len, rows, cols, X, ldx, logits, ldl, ids, batch, &g, &m, &al,
+                                   &max_cols))
+        return rc;
+    if (batch > kLmScratchTokens || (batch - 1) * ldl + rows > kLmScratchBndFloats) {
+        g_lm_err = "pyrite_dev_lm_head_argmax_noalloc: at most 8 vectors and (batch - 1) * ldl + rows <= "
+                   "1894336 (the fixed 8 MiB scratch)";
+        return -2;
+    }
+    void* base = nullptr;
+    if (const int rc = lm_scratch(&base)) return rc;
+    float* bnd = reinterpret_cast<float*>(static_cast<char*>(base) + kLmScratchBndOffset);
+    return lm_head_run(type, g, al, max_cols, m, ids, batch, bnd, base, kLmScratchTokens, true, stream);
 }
 
 }  // namespace pyrite
