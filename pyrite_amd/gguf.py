@@ -1,33 +1,46 @@
-"""Bounds-checked GGUF v2/v3 reader: the tensor directory the HBM loader uploads from.
+"""GGUF v2/v3 tensor directory for the HBM loader.
 
-Mirrors the public surface and error behaviour of the reference reader
-(pyrite/adapters/gguf.py:12-389): ``GGUFHeader``, ``GGUFTensor``,
-``GGUFError`` (a ``ValueError``), and ``GGUFReader`` with ``header()``,
-``metadata()``, ``get()``, ``tensor_index()``, ``tensor()``,
-``has_tensor()``, ``tensor_names()``, ``tensor_data_offset``,
-``size_bytes`` and ``read_tensor()``, the same safety limits and the same
-rejections (bad magic, v1 or > v3, absurd counts, strings longer than what
-remains, duplicate keys and names, names of 64+ bytes, more than 4 dims, zero
-dims, unknown block types, unaligned, out-of-file or overlapping payloads).
+Interface (kept so code written against the reference reader,
+pyrite/adapters/gguf.py, works unchanged): the dataclasses ``GGUFHeader`` and
+``GGUFTensor``, the exception ``GGUFError`` (a ``ValueError``), and
+``GGUFReader`` with ``header()``, ``metadata()``, ``get()``,
+``tensor_index()``, ``tensor()``, ``has_tensor()``, ``tensor_names()``,
+``tensor_data_offset``, ``size_bytes``, ``read_tensor()`` and the class limits
+``MAX_DIMS``, ``MAX_NAME``, ``MIN_VERSION``/``MAX_VERSION``, ``MAX_TENSORS``,
+``MAX_METADATA``, ``MAX_ARRAY``, ``MAX_STRING_BYTES`` and
+``DEFAULT_ALIGNMENT``.  Files are parsed lazily, on the first accessor call.
 
-The parse runs over a read-only memory map of the file: every field is
-decoded from the mapped bytes with explicit bounds, and arrays of fixed-width
-numbers (a 151936-entry token-score table, say) are decoded in one numpy
-call instead of element by element.  Parsing is lazy, as in the reference:
-nothing is read until an accessor is called.
+The file format (little-endian throughout):
+
+    "GGUF"  u32 version  u64 n_tensors  u64 n_kv
+    n_kv    x  { string key, u32 value type, value }
+    n_tensors x { string name, u32 n_dims, u64 dims[n_dims], u32 ggml type,
+                  u64 offset relative to the data section }
+    zero padding to the alignment (general.alignment, default 32)
+    tensor payloads
+
+with string = u64 byte length + UTF-8 bytes and array = u32 element type +
+u64 count + elements.  Version 1 used 32-bit counts and is not read.
+
+Parsing happens in two passes over a read-only memory map.  The first decodes
+the header, the key/value pairs and the directory records through ``_Span``,
+which refuses any read past the end of the file.  The second places the
+payloads: it computes each tensor's size from its GGML geometry, then checks
+alignment, extent and that no two payloads share a byte.  Fixed-width arrays,
+such as a 151936-entry token-score table, are decoded with one numpy call.
 """
 from __future__ import annotations
 
 import mmap
+import os
 import struct
 from dataclasses import dataclass
 from pathlib import Path
-from typing import Any
+from typing import Any, NamedTuple
 
 import numpy as np
 
 from .ggml_types import row_size
-from .ggml_types import spec as ggml_spec
 
 
 @dataclass(frozen=True)
@@ -41,7 +54,7 @@ class GGUFHeader:
 
 @dataclass(frozen=True)
 class GGUFTensor:
-    """One tensor of the directory; ``offset`` is absolute in the file."""
+    """A directory entry; ``offset`` is absolute in the file, ``size`` in bytes."""
     name: str
     dims: tuple[int, ...]
     ggml_type: int
@@ -54,288 +67,264 @@ class GGUFTensor:
 
     @property
     def element_count(self) -> int:
-        # unused GGML dimensions are 1, so a 0-dim tensor is one element
-        n = 1
-        for d in self.dims:
-            n *= d
-        return n
+        return int(np.prod(self.dims, dtype=object)) if self.dims else 1
 
 
 class GGUFError(ValueError):
-    """A GGUF file that cannot be parsed safely; the message names the field."""
+    """The file is not a GGUF checkpoint this reader can use; the message says why."""
 
 
-# GGUF metadata value types and the numpy dtype of the fixed-width ones.
-T_U8, T_I8, T_U16, T_I16, T_U32, T_I32, T_F32, T_BOOL = 0, 1, 2, 3, 4, 5, 6, 7
-T_STRING, T_ARRAY, T_U64, T_I64, T_F64 = 8, 9, 10, 11, 12
-_FIXED = {T_U8: "<u1", T_I8: "<i1", T_U16: "<u2", T_I16: "<i2", T_U32: "<u4", T_I32: "<i4",
-          T_F32: "<f4", T_U64: "<u8", T_I64: "<i8", T_F64: "<f8"}
+# Metadata value types: id -> (struct format, numpy dtype) for fixed-width ones.
+_U8, _I8, _U16, _I16, _U32, _I32, _F32, _BOOL, _STRING, _ARRAY, _U64, _I64, _F64 = range(13)
+_SCALARS: dict[int, tuple[str, str]] = {
+    _U8: ("<B", "<u1"), _I8: ("<b", "<i1"), _U16: ("<H", "<u2"), _I16: ("<h", "<i2"),
+    _U32: ("<I", "<u4"), _I32: ("<i", "<i4"), _F32: ("<f", "<f4"), _U64: ("<Q", "<u8"),
+    _I64: ("<q", "<i8"), _F64: ("<d", "<f8"),
+}
 
 
-class _Reader:
-    """Cursor over the mapped file; every read is checked against the end."""
+class _Span:
+    """Decoding position over the mapped bytes [0, end)."""
 
-    MAX_STRING_BYTES = 4 * 1024 * 1024
+    def __init__(self, mv: memoryview, end: int, string_cap: int):
+        self.mv = mv
+        self.at = 0
+        self.end = end
+        self.string_cap = string_cap
 
-    def __init__(self, buf, limit: int):
-        self.buf = buf
-        self.pos = 0
-        self.limit = limit
+    def left(self) -> int:
+        return self.end - self.at
 
-    @property
-    def remaining(self) -> int:
-        return max(0, self.limit - self.pos)
+    def bytes(self, n: int, what: str) -> bytes:
+        if n > self.left():
+            raise GGUFError(f"file ends at byte {self.end}: {what} needs {n} bytes from offset {self.at}")
+        out = bytes(self.mv[self.at:self.at + n])
+        self.at += n
+        return out
 
-    def take(self, n: int) -> bytes:
-        if n < 0:
-            raise GGUFError(f"negative GGUF read of {n} bytes")
-        if n > self.remaining:
-            raise GGUFError(f"truncated GGUF checkpoint: wanted {n} bytes at offset {self.pos}, "
-                            f"got {self.remaining}")
-        v = self.buf[self.pos:self.pos + n]  # a copy: no view of the map outlives the parse
-        self.pos += n
-        return v
+    def scalar(self, fmt: str, what: str):
+        return struct.unpack(fmt, self.bytes(struct.calcsize(fmt), what))[0]
 
-    def scalar(self, fmt: str):
-        return struct.unpack(fmt, self.take(struct.calcsize(fmt)))[0]
-
-    def u32(self) -> int:
-        return self.scalar("<I")
-
-    def u64(self) -> int:
-        return self.scalar("<Q")
-
-    def string(self, label: str = "string") -> str:
-        n = self.u64()
-        if n > self.remaining:
-            raise GGUFError(f"GGUF {label} claims {n} bytes but only {self.remaining} remain in the file")
-        if n > self.MAX_STRING_BYTES:
-            raise GGUFError(f"GGUF {label} length {n} exceeds the {self.MAX_STRING_BYTES}-byte safety limit")
+    def text(self, what: str) -> str:
+        start = self.at
+        n = self.scalar("<Q", f"the length of {what}")
+        if n > self.left():
+            raise GGUFError(f"{what} at offset {start} declares {n} bytes; only {self.left()} are left")
+        if n > self.string_cap:
+            raise GGUFError(f"{what} at offset {start} declares {n} bytes, over the {self.string_cap}-byte "
+                            "cap on strings")
+        raw = self.bytes(n, what)
         try:
-            return self.take(n).decode("utf-8")
+            return raw.decode("utf-8")
         except UnicodeDecodeError as exc:
-            raise GGUFError(f"invalid UTF-8 in GGUF {label}") from exc
+            raise GGUFError(f"{what} at offset {start} is not UTF-8") from exc
+
+
+class _Record(NamedTuple):
+    """A directory entry before its payload is placed."""
+    name: str
+    dims: tuple[int, ...]
+    ggml_type: int
+    rel: int
 
 
 class GGUFReader:
-    """Bounds-checked, lazy reader of GGUF v2-v3 checkpoints."""
+    """Lazy, bounds-checked reader of GGUF v2 and v3 checkpoints."""
 
     MAGIC = b"GGUF"
     DEFAULT_ALIGNMENT = 32   # GGUF_DEFAULT_ALIGNMENT
     MAX_DIMS = 4             # GGML_MAX_DIMS
-    MAX_NAME = 64            # GGML_MAX_NAME: names must be shorter
-    MIN_VERSION = 2          # v1 used 32-bit counts; refused
+    MAX_NAME = 64            # GGML_MAX_NAME (a name must be shorter)
+    MIN_VERSION = 2
     MAX_VERSION = 3
     MAX_TENSORS = 10_000_000
     MAX_METADATA = 1_000_000
     MAX_ARRAY = 100_000_000
-    MAX_STRING_BYTES = _Reader.MAX_STRING_BYTES
+    MAX_STRING_BYTES = 4 << 20
 
     def __init__(self, path: Path | str):
         self.path = Path(path)
-        self._parsed = False
-        self._header: GGUFHeader | None = None
-        self._metadata: dict[str, Any] = {}
-        self._tensors: tuple[GGUFTensor, ...] = ()
-        self._index: dict[str, GGUFTensor] = {}
-        self._size = 0
+        self._state: tuple[GGUFHeader, dict[str, Any], tuple[GGUFTensor, ...], int] | None = None
+        self._by_name: dict[str, GGUFTensor] = {}
 
-    # ------------------------------------------------------------ accessors
+    # ---------------------------------------------------------------- access
+    def _loaded(self):
+        if self._state is None:
+            self._state = self._load()
+            self._by_name = {t.name: t for t in self._state[2]}
+        return self._state
+
     def header(self) -> GGUFHeader:
-        self._ensure_parsed()
-        return self._header
+        return self._loaded()[0]
 
     def metadata(self) -> dict[str, Any]:
-        self._ensure_parsed()
-        return dict(self._metadata)
+        return dict(self._loaded()[1])
 
     def get(self, key: str, default: Any = None) -> Any:
-        self._ensure_parsed()
-        return self._metadata.get(key, default)
+        return self._loaded()[1].get(key, default)
 
     def tensor_index(self) -> tuple[GGUFTensor, ...]:
-        self._ensure_parsed()
-        return self._tensors
+        return self._loaded()[2]
 
     def tensor(self, name: str) -> GGUFTensor:
-        self._ensure_parsed()
-        try:
-            return self._index[name]
-        except KeyError as exc:
-            raise KeyError(f"missing GGUF tensor: {name}") from exc
+        self._loaded()
+        found = self._by_name.get(name)
+        if found is None:
+            raise KeyError(f"no tensor named {name!r} in {self.path.name}")
+        return found
 
     def has_tensor(self, name: str) -> bool:
-        self._ensure_parsed()
-        return name in self._index
+        self._loaded()
+        return name in self._by_name
 
     def tensor_names(self) -> tuple[str, ...]:
-        return tuple(t.name for t in self.tensor_index())
+        return tuple(t.name for t in self._loaded()[2])
 
     @property
     def tensor_data_offset(self) -> int:
-        self._ensure_parsed()
-        return self._header.data_offset
+        return self._loaded()[0].data_offset
 
     @property
     def size_bytes(self) -> int:
-        self._ensure_parsed()
-        return self._size
+        return self._loaded()[3]
 
     def read_tensor(self, tensor: GGUFTensor) -> bytes:
-        """The tensor's payload bytes, verbatim."""
-        self._ensure_parsed()
-        if tensor.offset < 0 or tensor.end > self._size:
-            raise ValueError(f"tensor {tensor.name!r} lies outside the checkpoint")
-        with self.path.open("rb") as fh:
-            fh.seek(tensor.offset)
-            data = fh.read(tensor.size)
+        """The payload bytes of ``tensor`` as stored (one positioned read)."""
+        size = self._loaded()[3]
+        if tensor.offset < 0 or tensor.size < 0 or tensor.end > size:
+            raise ValueError(f"{tensor.name!r} spans bytes [{tensor.offset}, {tensor.end}) of a {size}-byte file")
+        fd = os.open(self.path, os.O_RDONLY)
+        try:
+            data = os.pread(fd, tensor.size, tensor.offset)
+        finally:
+            os.close(fd)
         if len(data) != tensor.size:
-            raise ValueError(f"truncated tensor payload: {tensor.name}")
+            raise ValueError(f"{tensor.name!r}: read {len(data)} of {tensor.size} payload bytes")
         return data
 
-    def describe_type(self, ggml_type: int) -> str:
-        return ggml_spec(ggml_type).name
-
-    # ---------------------------------------------------------------- parse
-    def _ensure_parsed(self) -> None:
-        if self._parsed:
-            return
+    # ----------------------------------------------------------------- parse
+    def _load(self):
         if not self.path.is_file():
             raise FileNotFoundError(self.path)
         size = self.path.stat().st_size
-        with self.path.open("rb") as fh:
-            if size == 0:
-                raise GGUFError(f"not a GGUF checkpoint: {self.path.name} is empty (bad magic)")
-            with mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ) as mm:
-                self._parse(_Reader(mm, size), size)
-        self._parsed = True
-
-    def _parse(self, r: _Reader, size: int) -> None:
-        if r.take(4) != self.MAGIC:
-            raise GGUFError(f"not a GGUF checkpoint: bad magic in {self.path.name}")
-        version = r.u32()
-        if version < self.MIN_VERSION:
-            raise GGUFError(f"unsupported GGUF version {version}: GGUFv1 used 32-bit counts and is no "
-                            "longer supported by the reference implementation; re-export as v3")
-        if version > self.MAX_VERSION:
-            raise GGUFError(f"unsupported GGUF version {version}: readable versions are "
-                            f"v{self.MIN_VERSION}-v{self.MAX_VERSION}")
-        n_tensors, n_meta = r.u64(), r.u64()
-        if n_tensors > self.MAX_TENSORS or n_meta > self.MAX_METADATA:
-            raise GGUFError(f"GGUF header declares {n_tensors} tensors and {n_meta} metadata entries; the "
-                            f"safety limits are {self.MAX_TENSORS} and {self.MAX_METADATA}, so the file is "
-                            "corrupt or truncated")
-
-        metadata: dict[str, Any] = {}
-        alignment = self.DEFAULT_ALIGNMENT
-        for _ in range(n_meta):
-            key = r.string("metadata key")
-            vtype = r.u32()
-            if key in metadata:
-                raise GGUFError(f"duplicate GGUF metadata key: {key}")
-            value = self._value(r, vtype, key)
-            metadata[key] = value
-            if key == "general.alignment":
-                if isinstance(value, bool) or not isinstance(value, int) or value <= 0 or value & (value - 1):
-                    raise GGUFError(f"invalid GGUF alignment {value!r}: must be a positive power of two")
-                alignment = value
-
-        directory = []
-        names: set[str] = set()
-        for _ in range(n_tensors):
-            name = r.string("tensor name")
-            n_dims = r.u32()
-            if name in names:
-                raise GGUFError(f"duplicate GGUF tensor name: {name}")
-            if len(name) >= self.MAX_NAME:
-                raise GGUFError(f"tensor name {name[:32]!r}... is {len(name)} bytes; GGML_MAX_NAME is "
-                                f"{self.MAX_NAME}")
-            names.add(name)
-            if n_dims > self.MAX_DIMS:
-                raise GGUFError(f"GGUF tensor {name!r} has {n_dims} dimensions; GGML_MAX_DIMS is {self.MAX_DIMS}")
-            dims = tuple(int(d) for d in np.frombuffer(r.take(8 * n_dims), dtype="<u8"))
-            if any(d == 0 for d in dims):
-                raise GGUFError(f"GGUF tensor {name!r} has a zero-sized dimension: {dims}")
-            gtype = r.u32()
-            rel = r.u64()
-            directory.append((name, dims, gtype, rel))
-
-        # tensor data begins at the next multiple of the alignment
-        data_offset = -(-r.pos // alignment) * alignment if n_tensors else r.pos
-        if data_offset > size:
-            raise GGUFError(f"GGUF tensor data starts at {data_offset}, beyond the {size}-byte file")
-        tensors = []
-        for name, dims, gtype, rel in directory:
-            if rel % alignment:
-                raise GGUFError(f"unaligned GGUF tensor offset: {name} starts at {rel}, which is not a multiple "
-                                f"of the {alignment}-byte alignment")
+        if size < 4:
+            raise GGUFError(f"{self.path.name} has {size} bytes: too short for the GGUF magic")
+        with self.path.open("rb") as fh, mmap.mmap(fh.fileno(), 0, access=mmap.ACCESS_READ) as mm:
+            mv = memoryview(mm)
             try:
-                nbytes = self._tensor_size(dims, gtype, name)
-            except ValueError as exc:
-                raise GGUFError(str(exc)) from exc
-            if rel > size - data_offset:
-                raise GGUFError(f"GGUF tensor {name} offset {rel} lies beyond the file")
-            start = data_offset + rel
-            if nbytes > size - start:
-                raise GGUFError(f"GGUF tensor {name} needs {nbytes} bytes at {start} but the file ends at {size}")
-            tensors.append(GGUFTensor(name, dims, gtype, start, nbytes))
-        # payloads may appear in any order but must not overlap
-        last_end, last_name = data_offset, ""
-        for t in sorted(tensors, key=lambda t: (t.offset, t.end, t.name)):
-            if t.offset < last_end:
-                raise GGUFError(f"GGUF tensor payload overlaps another tensor: {last_name}, {t.name}")
-            last_end, last_name = t.end, t.name
+                version, kv, records, end_of_directory = self._decode(_Span(mv, size, self.MAX_STRING_BYTES))
+            finally:
+                mv.release()
+        alignment = self._alignment(kv)
+        data_offset = end_of_directory if not records else -(-end_of_directory // alignment) * alignment
+        if data_offset > size:
+            raise GGUFError(f"the data section would start at byte {data_offset}, past the end of the "
+                            f"{size}-byte file")
+        tensors = self._place(records, alignment, data_offset, size)
+        header = GGUFHeader(version, len(records), len(kv), alignment, data_offset)
+        return header, kv, tensors, size
 
-        self._header = GGUFHeader(version, n_tensors, n_meta, alignment, data_offset)
-        self._metadata = metadata
-        self._tensors = tuple(tensors)
-        self._index = {t.name: t for t in tensors}
-        self._size = size
+    def _decode(self, sp: _Span):
+        magic = sp.bytes(4, "the magic")
+        if magic != self.MAGIC:
+            raise GGUFError(f"{self.path.name}: first four bytes are {magic!r}, not the GGUF magic")
+        version = sp.scalar("<I", "the version")
+        if not self.MIN_VERSION <= version <= self.MAX_VERSION:
+            raise GGUFError(f"GGUF version {version} is not readable here (versions {self.MIN_VERSION} to "
+                            f"{self.MAX_VERSION} are; version 1 used 32-bit counts)")
+        n_tensors = sp.scalar("<Q", "the tensor count")
+        n_kv = sp.scalar("<Q", "the key/value count")
+        if n_tensors > self.MAX_TENSORS or n_kv > self.MAX_METADATA:
+            raise GGUFError(f"the header counts ({n_tensors} tensors, {n_kv} key/value pairs) exceed the "
+                            f"safety limits ({self.MAX_TENSORS}, {self.MAX_METADATA})")
+        kv: dict[str, Any] = {}
+        for i in range(n_kv):
+            key = sp.text(f"metadata key {i}")
+            if key in kv:
+                raise GGUFError(f"key {key!r} appears twice in the metadata")
+            vtype = sp.scalar("<I", f"the value type of {key!r}")
+            kv[key] = self._value(sp, vtype, key)
+        records: list[_Record] = []
+        seen: set[str] = set()
+        for i in range(n_tensors):
+            name = sp.text(f"tensor name {i}")
+            if len(name.encode()) >= self.MAX_NAME:
+                raise GGUFError(f"tensor name of {len(name.encode())} bytes ({name[:24]!r}...) is not shorter "
+                                f"than GGML_MAX_NAME = {self.MAX_NAME}")
+            if name in seen:
+                raise GGUFError(f"tensor {name!r} appears twice in the directory")
+            seen.add(name)
+            n_dims = sp.scalar("<I", f"the rank of {name!r}")
+            if n_dims > self.MAX_DIMS:
+                raise GGUFError(f"tensor {name!r} has {n_dims} dimensions; GGML allows at most {self.MAX_DIMS}")
+            dims = tuple(int(d) for d in np.frombuffer(sp.bytes(8 * n_dims, f"the shape of {name!r}"), "<u8"))
+            if 0 in dims:
+                raise GGUFError(f"tensor {name!r} has an empty dimension in {dims}")
+            gtype = sp.scalar("<I", f"the type of {name!r}")
+            rel = sp.scalar("<Q", f"the offset of {name!r}")
+            records.append(_Record(name, dims, gtype, rel))
+        return version, kv, records, sp.at
 
-    def _value(self, r: _Reader, vtype: int, key: str) -> Any:
-        if vtype in _FIXED:
-            dt = np.dtype(_FIXED[vtype])
-            v = np.frombuffer(r.take(dt.itemsize), dtype=dt)[0]
-            return float(v) if dt.kind == "f" else int(v)
-        if vtype == T_BOOL:
-            b = r.scalar("<B")
-            if b not in (0, 1):
-                raise GGUFError(f"invalid GGUF boolean value: {b}")
-            return bool(b)
-        if vtype == T_STRING:
-            return r.string(f"metadata value for {key!r}")
-        if vtype == T_ARRAY:
-            etype, count = r.u32(), r.u64()
+    def _value(self, sp: _Span, vtype: int, key: str) -> Any:
+        if vtype in _SCALARS:
+            v = sp.scalar(_SCALARS[vtype][0], f"the value of {key!r}")
+            return float(v) if isinstance(v, float) else int(v)
+        if vtype == _BOOL:
+            return self._bools(sp.bytes(1, f"the value of {key!r}"))[0]
+        if vtype == _STRING:
+            return sp.text(f"the value of {key!r}")
+        if vtype == _ARRAY:
+            etype = sp.scalar("<I", f"the element type of {key!r}")
+            count = sp.scalar("<Q", f"the element count of {key!r}")
             if count > self.MAX_ARRAY:
-                raise GGUFError(f"GGUF metadata array {key!r} declares {count} elements, above the "
-                                f"{self.MAX_ARRAY} safety limit")
-            # every element takes at least one byte: a larger count cannot be real
-            if count > r.remaining:
-                raise GGUFError(f"GGUF metadata array {key!r} declares {count} elements but only "
-                                f"{r.remaining} bytes remain in the file")
-            if etype in _FIXED:
-                dt = np.dtype(_FIXED[etype])
-                arr = np.frombuffer(r.take(count * dt.itemsize), dtype=dt)
-                return tuple(arr.tolist())
-            if etype == T_BOOL:
-                raw = np.frombuffer(r.take(count), dtype=np.uint8)
-                bad = raw[raw > 1]
-                if bad.size:
-                    raise GGUFError(f"invalid GGUF boolean value: {int(bad[0])}")
-                return tuple(bool(b) for b in raw)
-            return tuple(self._value(r, etype, key) for _ in range(count))
-        raise GGUFError(f"unsupported GGUF metadata value type {vtype} for key {key!r}")
+                raise GGUFError(f"array {key!r} declares {count} elements, over the {self.MAX_ARRAY}-element cap")
+            if count > sp.left():  # every element takes at least one byte
+                raise GGUFError(f"array {key!r} declares {count} elements; only {sp.left()} bytes are left")
+            if etype in _SCALARS:
+                dt = np.dtype(_SCALARS[etype][1])
+                return tuple(np.frombuffer(sp.bytes(count * dt.itemsize, f"the elements of {key!r}"), dt).tolist())
+            if etype == _BOOL:
+                return self._bools(sp.bytes(count, f"the elements of {key!r}"))
+            return tuple(self._value(sp, etype, key) for _ in range(count))
+        raise GGUFError(f"key {key!r} has value type {vtype}, which GGUF does not define")
 
     @staticmethod
-    def _tensor_size(dims: tuple[int, ...], ggml_type: int, name: str = "") -> int:
-        """Payload bytes: rows of dims[0] elements times the product of the other dims."""
-        if not dims:
-            return row_size(1, ggml_type)
-        rows = 1
-        for d in dims[1:]:
-            rows *= d
-        try:
-            return row_size(dims[0], ggml_type) * rows
-        except (TypeError, ValueError) as exc:
-            label = f"tensor {name!r}: " if name else ""
-            raise ValueError(f"{label}{exc}") from exc
+    def _bools(raw: bytes) -> tuple[bool, ...]:
+        arr = np.frombuffer(raw, np.uint8)
+        if (arr > 1).any():
+            raise GGUFError(f"boolean value byte {int(arr[arr > 1][0])} is neither 0 nor 1")
+        return tuple(bool(b) for b in arr)
+
+    def _alignment(self, kv: dict[str, Any]) -> int:
+        a = kv.get("general.alignment", self.DEFAULT_ALIGNMENT)
+        if isinstance(a, bool) or not isinstance(a, int) or a <= 0 or a & (a - 1):
+            raise GGUFError(f"general.alignment = {a!r} is not a positive power of two")
+        return a
+
+    @staticmethod
+    def _place(records: list[_Record], alignment: int, data_offset: int, size: int) -> tuple[GGUFTensor, ...]:
+        room = size - data_offset
+        placed = []
+        for r in records:
+            if r.rel % alignment:
+                raise GGUFError(f"tensor {r.name!r}: payload offset {r.rel} is not a multiple of the "
+                                f"{alignment}-byte alignment")
+            # bytes = rows of dims[0] elements x the other dims (a 0-D tensor is one element)
+            try:
+                nbytes = row_size(r.dims[0] if r.dims else 1, r.ggml_type)
+            except (TypeError, ValueError) as exc:
+                raise GGUFError(f"tensor {r.name!r}: {exc}") from exc
+            for d in r.dims[1:]:
+                nbytes *= d
+            if r.rel > room:
+                raise GGUFError(f"tensor {r.name!r}: payload offset {r.rel} is past the end of the data section")
+            if nbytes > room - r.rel:
+                raise GGUFError(f"tensor {r.name!r}: {nbytes} payload bytes from byte {data_offset + r.rel} run "
+                                f"past the end of the file ({size} bytes)")
+            placed.append(GGUFTensor(r.name, r.dims, r.ggml_type, data_offset + r.rel, nbytes))
+        # payloads may be stored in any order, but no byte may belong to two tensors
+        by_start = sorted(placed, key=lambda t: (t.offset, t.end))
+        for a, b in zip(by_start, by_start[1:]):
+            if b.offset < a.end:
+                raise GGUFError(f"payloads of tensors {a.name!r} and {b.name!r} overlap")
+        return tuple(placed)

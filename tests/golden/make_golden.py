@@ -32,9 +32,8 @@ import numpy as np
 ROOT = Path(__file__).resolve().parents[2]
 sys.path.insert(0, str(ROOT))
 
-from oracle.oracle import (  # noqa: E402
-    TYPES, finite_bf16words, finite_halfwords, lcg_payload, oracle, reference,
-)
+from oracle.oracle import TYPES, lcg_payload, oracle, reference  # noqa: E402
+from tests.gpu_util import HALF_WORDS, random_payload  # noqa: E402
 
 OUT = Path(__file__).resolve().parent
 REFERENCE_TESTS = Path("/root/reference/tests")
@@ -43,34 +42,8 @@ REFERENCE_TESTS = Path("/root/reference/tests")
 SPECIAL_HALVES = [0x0000, 0x8000, 0x0001, 0x03FF, 0x0400, 0x7BFF, 0xBC00, 0x3C00,
                   0x0200, 0x8001, 0xFBFF, 0x1400, 0x2E66, 0xB555]
 
-# byte offsets of fp16 words inside one block (scale, min, sum words)
-HALF_WORDS = {1: (0,), 2: (0,), 3: (0, 2), 6: (0,), 7: (0, 2), 8: (0,), 9: (0, 2),
-              10: (80, 82), 11: (108,), 12: (0, 2), 13: (0, 2), 14: (208,), 20: (0,),
-              23: (0,), 30: (0,)}
-
-
 def ref_vector(cols: int) -> np.ndarray:
     return np.array([math.cos(i * 0.13) * 0.4 for i in range(cols)], dtype=np.float64)
-
-
-def random_payload(rng, type_id: int, rows: int, cols: int) -> np.ndarray:
-    name, bs, bpb = TYPES[type_id]
-    if type_id == 0:
-        return rng.standard_normal(rows * cols).astype("<f4").view(np.uint8).copy()
-    if type_id == 28:
-        return rng.standard_normal(rows * cols).astype("<f8").view(np.uint8).copy()
-    raw = rng.integers(0, 256, size=rows * (cols // bs) * bpb, dtype=np.uint8)
-    if type_id == 30:
-        return finite_bf16words(raw)
-    if type_id == 1:
-        return finite_halfwords(raw)
-    # keep block scale words finite so the outputs are comparable numbers
-    for blk in range(raw.size // bpb):
-        for off in HALF_WORDS.get(type_id, ()):
-            w = int(raw[blk * bpb + off]) | (int(raw[blk * bpb + off + 1]) << 8)
-            if (w & 0x7C00) == 0x7C00:
-                raw[blk * bpb + off + 1] &= 0x3B
-    return raw
 
 
 def special_payload(rng, type_id: int, rows: int, cols: int) -> np.ndarray:

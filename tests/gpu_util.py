@@ -1,9 +1,38 @@
-"""Helpers shared by the GPU parity tests (imported only by tests marked gpu)."""
+"""Helpers shared by the parity tests and the fixture script (no GPU, no torch here)."""
 from __future__ import annotations
 
 import sys
 
 import numpy as np
+
+from oracle.oracle import TYPES, finite_bf16words, finite_halfwords
+
+# byte offsets of fp16 words inside one block (scale, min, sum words)
+HALF_WORDS = {1: (0,), 2: (0,), 3: (0, 2), 6: (0,), 7: (0, 2), 8: (0,), 9: (0, 2),
+              10: (80, 82), 11: (108,), 12: (0, 2), 13: (0, 2), 14: (208,), 20: (0,),
+              23: (0,), 30: (0,)}
+
+
+def random_payload(rng, type_id: int, rows: int, cols: int) -> np.ndarray:
+    """Random block bytes (every code, scale and bit pattern) with the fp16 words
+    that scale a block kept finite, so that outputs are comparable numbers."""
+    _, bs, bpb = TYPES[type_id]
+    if type_id == 0:
+        return rng.standard_normal(rows * cols).astype("<f4").view(np.uint8).copy()
+    if type_id == 28:
+        return rng.standard_normal(rows * cols).astype("<f8").view(np.uint8).copy()
+    raw = rng.integers(0, 256, size=rows * (cols // bs) * bpb, dtype=np.uint8)
+    if type_id == 30:
+        return finite_bf16words(raw)
+    if type_id == 1:
+        return finite_halfwords(raw)
+    for blk in range(raw.size // bpb):
+        for off in HALF_WORDS.get(type_id, ()):
+            w = int(raw[blk * bpb + off]) | (int(raw[blk * bpb + off + 1]) << 8)
+            if (w & 0x7C00) == 0x7C00:
+                raw[blk * bpb + off + 1] &= 0x3B
+    return raw
+
 
 # Sizes and seeds named by every parity case, printed before the GPU step so a
 # failing run identifies its case from the log alone.

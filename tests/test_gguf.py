@@ -12,7 +12,7 @@ import struct
 import numpy as np
 import pytest
 
-from pyrite_amd.gguf import GGUFError, GGUFReader, _Reader
+from pyrite_amd.gguf import GGUFError, GGUFReader
 from tests import gguf_writer as gw
 
 
@@ -42,7 +42,7 @@ def test_valid_file_header_and_directory(tmp_path):
     assert r.get("general.architecture") == "qwen3" and r.get("qwen3.embedding_length") == 8
     assert r.tensor_names() == ("blk.0.attn_norm.weight",) and r.has_tensor("blk.0.attn_norm.weight")
     assert r.size_bytes == (tmp_path / "candidate.gguf").stat().st_size
-    with pytest.raises(KeyError, match="missing GGUF tensor"):
+    with pytest.raises(KeyError, match="no tensor named"):
         r.tensor("nope")
 
 
@@ -114,7 +114,7 @@ def test_overlapping_payloads_are_rejected(tmp_path):
     w = gw.Writer()
     w.tensor("a", (16,), 0, bytes(64), offset=0)
     w.tensor("b", (16,), 0, bytes(64), offset=32)
-    with pytest.raises(GGUFError, match="overlaps"):
+    with pytest.raises(GGUFError, match="'a' and 'b' overlap"):
         parse(tmp_path, w.bytes())
 
 
@@ -140,13 +140,14 @@ def test_version_two_is_accepted(tmp_path):
 
 
 @pytest.mark.parametrize("case, match", [
-    ("magic", "magic"), ("empty", None), ("short", None), ("v1", "version"), ("v4", "version"),
-    ("neg_count", "safety limits"), ("many_tensors", "safety limits"), ("many_meta", "safety limits"),
-    ("truncated", "file ends at"), ("huge_string", "remain in the file"), ("string_past_end", "remain in the file"),
-    ("long_name", "name"), ("dup_key", "duplicate"), ("dup_tensor", "duplicate"), ("dims", "dimension"),
-    ("zero_dim", "zero-sized"), ("type", "type"), ("offset", "beyond the file"), ("unaligned", "unaligned"),
-    ("alignment", "alignment"), ("bool", "boolean"), ("array_count", "remain in the file"),
-    ("value_type", "value type"),
+    ("magic", "magic"), ("empty", "too short"), ("short", "file ends at"), ("v1", "version 1 "),
+    ("v4", "version 4 "), ("neg_count", "safety limits"), ("many_tensors", "safety limits"),
+    ("many_meta", "safety limits"), ("truncated", "past the end of the file"), ("huge_string", r"declares \d+ bytes; only \d+ are left"),
+    ("string_past_end", r"declares 1099511627776 bytes; only"), ("long_name", "GGML_MAX_NAME"), ("dup_key", "twice in the metadata"),
+    ("dup_tensor", "twice in the directory"), ("dims", "at most 4"), ("zero_dim", "empty dimension"),
+    ("type", "unsupported GGML tensor type"), ("offset", "past the end of the data section"),
+    ("unaligned", "not a multiple"), ("alignment", "power of two"), ("bool", "neither 0 nor 1"),
+    ("array_count", "bytes are left"), ("value_type", "does not define"),
 ])
 def test_malformed_files_are_rejected(tmp_path, case, match):
     w = good()
@@ -171,7 +172,7 @@ def test_malformed_files_are_rejected(tmp_path, case, match):
     elif case == "truncated":
         kw = {"truncate": 16}
     elif case == "huge_string":
-        w.raw_kv("general.name", gw.STRING, struct.pack("<Q", _Reader.MAX_STRING_BYTES + 1) + b"x")
+        w.raw_kv("general.name", gw.STRING, struct.pack("<Q", GGUFReader.MAX_STRING_BYTES + 1) + b"x")
     elif case == "string_past_end":
         w.raw_kv("general.name", gw.STRING, struct.pack("<Q", 1 << 40))
     elif case == "long_name":
@@ -226,3 +227,12 @@ def test_resident_tensors_need_a_gpu_device(tmp_path):
     r = parse(tmp_path, good().bytes())
     with pytest.raises(ValueError, match="CUDA"):
         ResidentTensors(r, device="cpu")
+
+
+def test_string_cap_is_enforced(tmp_path):
+    """A string longer than MAX_STRING_BYTES is refused even when the file holds it."""
+    w = good()
+    n = GGUFReader.MAX_STRING_BYTES + 1
+    w.raw_kv("general.name", gw.STRING, struct.pack("<Q", n) + b"x" * n)
+    with pytest.raises(GGUFError, match="cap on strings"):
+        parse(tmp_path, w.bytes())

@@ -238,7 +238,7 @@ QUANT_TYPES = [t for t in ALL_TYPES if TYPES[t][1] > 1]
 def _random_payload(t, rows, cols, seed):
     """Random block bytes (every code, scale and bit pattern) with the fp16
     block scale words kept finite, as in the reference's own kernel test."""
-    from tests.golden.make_golden import random_payload
+    from tests.gpu_util import random_payload
 
     return random_payload(np.random.default_rng(seed), t, rows, cols)
 

@@ -32,7 +32,7 @@ def _row_maxabs(orc, t, payload, rows, cols):
 
 
 def _random_q(rng, t, rows, cols):
-    from tests.golden.make_golden import random_payload
+    from tests.gpu_util import random_payload
     return random_payload(rng, t, rows, cols)
 
 

@@ -28,7 +28,7 @@ def dev():
 
 
 def _payload(rng, t, n_rows, cols):
-    from tests.golden.make_golden import random_payload
+    from tests.gpu_util import random_payload
     return random_payload(rng, t, n_rows, cols)
 
 
