@@ -1,32 +1,33 @@
 #!/usr/bin/env python3
 """Benchmark of the fused GGML dequantize x matvec path on one MI355X.
 
-Workload (the metric's configuration): every Qwen3-0.6B decode projection
-(hidden 1024, 16 q / 8 kv heads x head_dim 128: q 2048x1024, k/v 1024x1024,
-o 1024x2048, gate/up 3072x1024, down 1024x3072), each quantized from seeded
-N(0, 0.02) fp32 weights to Q4_0, Q5_1, Q8_0, Q3_K, Q5_K, Q6_K and IQ4_XS, with
-fp32 N(0, 1) activations at batch 1 and 8.
+Headline workload (value, roofline): the batch-1 decode of one Llama-3-8B
+layer in the Q4_K_M mix -- attn q/o 4096x4096 and k/v 1024x4096, ffn gate/up
+14336x4096 in Q4_K, ffn down 4096x14336 in Q6_K (137.8 MB of quantized
+weights), each quantized from seeded N(0, 0.02) fp32 weights, with fp32
+N(0, 1) activations.  One step is the layer's four launches in executor
+order: q/k/v grouped (pyrite_dev_matvec_grouped), o, gate/up grouped, down.
+Weights are uploaded verbatim and rotated over 3 device copies (413 MB > the
+256 MB Infinity Cache), so every launch reads its weights from HBM.  The
+timed steps are captured into one HIP graph and replayed once between two
+synchronisations.  value = quantized weight bytes / second over the timed
+steps (GB/s).  Each launch's duration for the roofline comes from HIP events
+that the launch itself records at kernel start and end (hipExtLaunchKernelGGL),
+over the same launches replayed eagerly on the same stream.
 
-One step = for batch in (1, 8), for each type: one grouped launch
-(pyrite_dev_matvec_grouped) over that type's 7 projection matrices.  Weights
-are uploaded verbatim and rotated over 4 device copies (305 MB > the 256 MB
-Infinity Cache), so every launch reads its weights from HBM.  The timed steps
-are captured into one HIP graph and replayed once between two
-synchronisations.  Each kernel's duration for the roofline comes from HIP
-events that the launch itself records at kernel start and end
-(hipExtLaunchKernelGGL), over the same launches replayed eagerly on the same
-stream right after the timed replay.
+Under "workloads", every other configuration of the path, each with its own
+roofline object: the single Q4_K 3072x1024 matvec, the Qwen3-0.6B projection
+type sweep (7 types x 7 projections, batch 1 and 8), the Q6_K 151936x1024 LM
+head with its exact greedy id, the Qwen3-30B-A3B MoE layer (tokens/s at batch
+1, 8, 64; also at top level), the Llama-3-8B layer's matrices alone at batch 1
+and its 512-token prefill (MFMA dequant-GEMM, against the fp16 matrix-core
+peak), and the GGUF -> HBM upload rate of the resident-tensor loader.
 
-Prints one JSON line.  value = quantized weight bytes / second over the timed
-steps (GB/s).  --gpus N > 1 exits: this path runs on one GPU.
+cpu_baseline: the reference's own native.c (oracle/_ref, built from the
+reference source) timed on the host on a bounded sample of the headline
+workload (whole decode layers, 7 single-vector pyrite_matvec calls each).
 
-The line also carries, under "workloads", the other workloads of the
-path, each timed as calls captured in one HIP graph: the single Q4_K
-3072x1024 matvec, the Q6_K 151936x1024 LM head with its exact greedy id, the
-Qwen3-30B-A3B MoE layer (tokens/s at batch 1, 8, 64) and the Llama-3-8B
-Q4_K_M layer (batch-1 decode and 512-token prefill; its q, gate and down
-matrices also alone at batch 1), and the GGUF -> HBM upload rate of the
-resident-tensor loader.
+Prints one JSON line.  --gpus N > 1 exits: this path runs on one GPU.
 """
 from __future__ import annotations
 
@@ -44,6 +45,13 @@ if str(ROOT) not in sys.path:
     sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 matrix-core peak (the dequant-GEMM runs f16 MFMAs)
+LLAMA = [("q", 12, 4096, 4096), ("k", 12, 1024, 4096), ("v", 12, 1024, 4096), ("o", 12, 4096, 4096),
+         ("gate", 12, 14336, 4096), ("up", 12, 14336, 4096), ("down", 14, 4096, 14336)]
+# the decode step's launches: (name, type, matrices, activation)
+DECODE_LAUNCHES = [("qkv", 12, ("q", "k", "v"), "normed"), ("o", 12, ("o",), "attn"),
+                   ("gate_up", 12, ("gate", "up"), "normed2"), ("down", 14, ("down",), "act")]
+DECODE_COPIES = 3
 SWEEP_TYPES = [("Q4_0", 2), ("Q5_1", 7), ("Q8_0", 8), ("Q3_K", 11), ("Q5_K", 13), ("Q6_K", 14), ("IQ4_XS", 23)]
 PROJECTIONS = [("q", 2048, 1024), ("k", 1024, 1024), ("v", 1024, 1024), ("o", 1024, 2048),
                ("gate", 3072, 1024), ("up", 3072, 1024), ("down", 1024, 3072)]
@@ -76,26 +84,40 @@ def cpu_info() -> tuple[str, int]:
     return model, os.cpu_count() or 1
 
 
-def build_weights(torch, np, quantize):
-    """Quantized sweep weights on the device: {type: [(rows, cols, tensor[COPIES])]}."""
-    rng = np.random.default_rng(SEED)
-    out = {}
-    total = 0
-    for name, t in SWEEP_TYPES:
-        mats = []
-        for pname, rows, cols in PROJECTIONS:
-            w = (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.02)).astype(np.float64)
-            payload = quantize(t, w)
-            base = torch.from_numpy(payload).to("cuda")
-            copies = [base] + [base.clone() for _ in range(COPIES - 1)]
-            mats.append((rows, cols, payload, copies))
-            total += payload.nbytes
-        out[t] = mats
-    return out, total
+def roofline_hbm(nbytes: float, avg_s: float, traffic=None, **extra) -> dict:
+    """Roofline object of an HBM-bound launch: algorithmic bytes per launch / its average duration."""
+    gbs = nbytes / avg_s / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "bytes_per_launch": int(nbytes),
+            "avg_launch_us": round(avg_s * 1e6, 3), **extra}
 
 
-def run_cpu_baseline(weights, np, budget_s: float):
-    """Time the reference's scalar fp64 pyrite_matvec on the host over the sweep."""
+def load_traffic(profile: str, key: str):
+    """HBM bytes per launch of `key` from a committed FETCH_SIZE / WRITE_SIZE
+    summary (profiles/<profile>.json), or None."""
+    try:
+        data = json.loads((ROOT / "profiles" / f"{profile}.json").read_text())
+    except (OSError, ValueError):
+        return None
+    entry = data.get("launches", {}).get(key)
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
+def llama_weights(np, quantize):
+    """The Llama-3-8B layer's matrices {name: (type, rows, cols, payload)}; matrices of
+    one shape and type share their seeded weights (q/o, k/v, gate/up)."""
+    cache, out = {}, {}
+    for name, t, rows, cols in LLAMA:
+        key = (t, rows, cols)
+        if key not in cache:
+            cache[key] = quantized_normal(np, quantize, t, rows * cols, SEED + 20 + len(cache))
+        out[name] = (t, rows, cols, cache[key])
+    return out
+
+
+def run_cpu_baseline(calls, budget_s: float, what: str):
+    """Time the reference's scalar fp64 pyrite_matvec on one host core over
+    `calls` [(type, payload, x, rows, cols)], repeated until budget_s passes."""
     from oracle.oracle import oracle, reference
 
     impl = reference()
@@ -103,46 +125,33 @@ def run_cpu_baseline(weights, np, budget_s: float):
     if impl is None:
         impl = oracle()
         kind = "port"
-    rng = np.random.default_rng(SEED + 7)
-    xs = {cols: rng.standard_normal((8, cols)) for cols in {c for _, _, c in PROJECTIONS}}
     done_bytes = 0
     passes = 0
     t0 = time.perf_counter()
     while True:
-        for _, t in SWEEP_TYPES:
-            for rows, cols, payload, _ in weights[t]:
-                for batch in BATCHES:
-                    for b in range(batch):
-                        impl.matvec(t, payload, xs[cols][b], rows, cols)
-                        done_bytes += payload.nbytes
+        for t, payload, x, rows, cols in calls:
+            impl.matvec(t, payload, x, rows, cols)
+            done_bytes += payload.nbytes
         passes += 1
         if time.perf_counter() - t0 >= budget_s:
             break
     dt = time.perf_counter() - t0
     return {"value": done_bytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{passes} pass(es) of the full sweep (7 types x 7 projections, batch 1 and 8 as 1+8 "
-                      f"single-vector calls) through pyrite_matvec, single thread, {dt:.1f} s"}
+            "sample": f"{passes} pass(es) of {what} through pyrite_matvec, single thread, {dt:.1f} s"}
 
 
-def run_cpu_baseline_parallel(weights, np, budget_s: float, nthreads: int):
-    """The same sweep on all host cores: thread i runs every call of the sweep
-    on its own contiguous i-th share of each matrix's rows (the reference
-    function is reentrant and rows are independent), so the threads never
-    wait for each other; throughput = all threads' bytes over the wall time."""
+def run_cpu_baseline_parallel(calls, budget_s: float, nthreads: int, what: str):
+    """The same calls on several host cores: thread i runs every call on its own
+    contiguous i-th share of each matrix's rows (the reference function is
+    reentrant and rows are independent), so the threads never wait for each
+    other; throughput = all threads' bytes over the wall time."""
     import threading
+
+    import numpy as np
 
     from oracle.oracle import oracle, reference
 
     impl = reference() or oracle()
-    rng = np.random.default_rng(SEED + 7)
-    xs = {cols: rng.standard_normal((8, cols)) for cols in {c for _, _, c in PROJECTIONS}}
-    calls = []
-    for _, t in SWEEP_TYPES:
-        for rows, cols, payload, _ in weights[t]:
-            rb = payload.nbytes // rows
-            for batch in BATCHES:
-                for b in range(batch):
-                    calls.append((t, payload, rb, xs[cols][b], rows, cols))
     done = [0] * nthreads
     passes = [0] * nthreads
     errors = []
@@ -153,7 +162,8 @@ def run_cpu_baseline_parallel(weights, np, budget_s: float, nthreads: int):
         outs = {}
         start.wait()
         while True:
-            for t, payload, rb, x, rows, cols in calls:
+            for t, payload, x, rows, cols in calls:
+                rb = payload.nbytes // rows
                 r0, r1 = rows * i // nthreads, rows * (i + 1) // nthreads
                 if r1 <= r0:
                     continue
@@ -178,8 +188,37 @@ def run_cpu_baseline_parallel(weights, np, budget_s: float, nthreads: int):
     if errors:
         raise ValueError("pyrite_matvec failed")
     return {"value": sum(done) / dt / 1e9, "unit": "GB/s", "cores": nthreads,
-            "sample": f"{min(passes)}-{max(passes)} pass(es) of the same sweep per thread, thread i on its "
-                      f"i-th share of every matrix's rows, {nthreads} threads, {dt:.1f} s"}
+            "sample": f"{min(passes)}-{max(passes)} pass(es) of {what} per thread, thread i on its i-th share "
+                      f"of every matrix's rows, {nthreads} threads, {dt:.1f} s"}
+
+
+def timed_grouped(lib, stream, sptr, launches, steps):
+    """Average kernel seconds of each grouped launch: launches = [(key, type, desc arrays per step
+    (callable s -> (array, n)), batch)], run eagerly for `steps` steps, each timed by HIP events
+    that the launch itself records at kernel start and end (pyrite_dev_matvec_grouped_timed)."""
+    import torch
+
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in launches]
+    for pair in evs:
+        for e in pair:
+            e.record(stream)  # creates the underlying hipEvent_t
+    torch.cuda.synchronize()
+    durations = {key: [] for key, *_ in launches}
+    for s in range(steps):
+        for k, (key, t, descs, batch) in enumerate(launches):
+            arr, n = descs(s)
+            rc = lib.pyrite_dev_matvec_grouped_timed(t, arr, n, batch, sptr, ctypes.c_void_p(evs[k][0].cuda_event),
+                                                     ctypes.c_void_p(evs[k][1].cuda_event))
+            if rc != 0:
+                raise RuntimeError(f"timed launch {key} failed: {rc} {lib.pyrite_hip_last_error()}")
+        torch.cuda.synchronize()
+        for k, (key, *_) in enumerate(launches):
+            durations[key].append(evs[k][0].elapsed_time(evs[k][1]) * 1e-3)
+    return {key: sum(d) / len(d) for key, d in durations.items()}
+
+
+TIMING = ("HIP events recorded by each launch at kernel start/end (hipExtLaunchKernelGGL), same launches "
+          "and weight rotation as the timed graph, on the same stream")
 
 
 # ---------------------------------------------------------------- other configurations
@@ -232,20 +271,9 @@ def copy_calibration(torch, stream):
 
 
 def launch_kernel_name(batch: int) -> str:
-    """Kernel that pyrite_dev_matvec_grouped runs for this type and batch (block formats)."""
-    return "mx_kernel (MFMA)" if batch >= 3 else "mv_kernel (VALU)"
-
-
-def load_traffic(key: str):
-    """HBM bytes per launch of a sweep launch ("<type>_b<batch>") from the committed
-    FETCH_SIZE / WRITE_SIZE profile (profiles/traffic_sweep.json), or None."""
-    path = ROOT / "profiles" / "traffic_sweep.json"
-    try:
-        data = json.loads(path.read_text())
-    except (OSError, ValueError):
-        return None
-    entry = data.get("launches", {}).get(key)
-    return None if entry is None else entry.get("hbm_bytes_per_launch")
+    """Kernel that a grouped launch of a block format runs at this batch."""
+    return "mg_kernel (MFMA dequant-GEMM)" if batch >= 64 else "mx_kernel (MFMA)" if batch >= 3 else \
+        "mv_kernel (VALU)"
 
 
 def bench_gguf_upload(torch, np):
@@ -326,7 +354,17 @@ def bench_gguf_upload(torch, np):
             "first_call_seconds": round(times[0], 4)}
 
 
-def bench_q4k_single(torch, np, quantize, stream, device):
+def _descs(np, mats, x, ys, copies=None):
+    """A Desc array over mats [(t, rows, cols, payload)] with device weights `copies`
+    (or their first copy), input x [batch, cols] and outputs ys."""
+    arr = (Desc * len(mats))()
+    for i, ((t, rows, cols, payload), w, y) in enumerate(zip(mats, copies, ys)):
+        arr[i] = Desc(w.data_ptr(), payload.nbytes, rows, cols, x.data_ptr(), x.stride(0) if x.shape[0] > 1 else cols,
+                      y.data_ptr(), y.stride(0) if y.shape[0] > 1 else rows)
+    return arr
+
+
+def bench_q4k_single(torch, np, quantize, lib, stream, sptr, device):
     """Single Q4_K 3072x1024 matvec (Qwen3-0.6B ffn_up), batch 1."""
     rows, cols = 3072, 1024
     p = quantized_normal(np, quantize, 12, rows * cols, SEED + 11)
@@ -335,11 +373,72 @@ def bench_q4k_single(torch, np, quantize, stream, device):
     y = torch.empty(1, rows, device="cuda")
     calls = [lambda w=w: device.matvec(12, w, x, rows, cols, out=y) for w in ws]
     dt = time_graph(torch, stream, calls)
+    arrs = [_descs(np, [(12, rows, cols, p)], x, [y], [w]) for w in ws]
+    avg = timed_grouped(lib, stream, sptr, [("q4k", 12, lambda s: (arrs[s % len(arrs)], 1), 1)], len(arrs))["q4k"]
     return {"workload": "Q4_K 3072x1024 matvec, batch 1", "us": round(dt * 1e6, 3),
-            "gbs": round(p.nbytes / dt / 1e9, 1), "pct_hbm_peak": round(100 * p.nbytes / dt / 1e9 / HBM_PEAK_GBS, 2)}
+            "gbs": round(p.nbytes / dt / 1e9, 1), "pct_hbm_peak": round(100 * p.nbytes / dt / 1e9 / HBM_PEAK_GBS, 2),
+            "roofline": roofline_hbm(p.nbytes, avg, load_traffic("traffic_configs", "q4k_3072x1024"),
+                                     kernel="mv_kernel (VALU) Q4_K batch 1", timing=TIMING)}
 
 
-def bench_lm_head(torch, np, quantize, stream, device):
+def bench_sweep(torch, np, quantize, lib, stream, sptr, steps: int):
+    """Qwen3-0.6B projection type sweep: one grouped launch of the 7 projections per type and batch."""
+    rng = np.random.default_rng(SEED)
+    weights = {}
+    for _, t in SWEEP_TYPES:
+        mats = []
+        for _, rows, cols in PROJECTIONS:
+            w = (rng.standard_normal(rows * cols, dtype=np.float32) * np.float32(0.02)).astype(np.float64)
+            payload = quantize(t, w)
+            base = torch.from_numpy(payload).cuda()
+            mats.append(((t, rows, cols, payload), [base] + [base.clone() for _ in range(COPIES - 1)]))
+        weights[t] = mats
+    xs = {(cols, b): torch.randn(b, cols, device="cuda") for cols in {c for _, _, c in PROJECTIONS} for b in BATCHES}
+    ys = {(t, i, b): torch.empty(b, rows, device="cuda")
+          for _, t in SWEEP_TYPES for i, (_, rows, _c) in enumerate(PROJECTIONS) for b in BATCHES}
+    descs = {}
+    for _, t in SWEEP_TYPES:
+        for b in BATCHES:
+            for c in range(COPIES):
+                arr = (Desc * len(PROJECTIONS))()
+                for i, ((tt, rows, cols, payload), copies) in enumerate(weights[t]):
+                    x, y = xs[(cols, b)], ys[(t, i, b)]
+                    arr[i] = Desc(copies[c].data_ptr(), payload.nbytes, rows, cols, x.data_ptr(), cols,
+                                  y.data_ptr(), rows)
+                descs[(t, b, c)] = arr
+    launches = [(t, b) for b in BATCHES for _, t in SWEEP_TYPES]
+
+    def step(s):
+        for t, b in launches:
+            rc = lib.pyrite_dev_matvec_grouped(t, descs[(t, b, (2 * s + BATCHES.index(b)) % COPIES)],
+                                               len(PROJECTIONS), b, sptr)
+            if rc != 0:
+                raise RuntimeError(f"sweep launch ({t}, {b}) failed: {rc} {lib.pyrite_hip_last_error()}")
+    dt = time_graph(torch, stream, [lambda s=s: step(s) for s in range(steps)],
+                    check=lambda: [y.clone() for y in ys.values()])
+    bytes_per_set = sum(m[0][3].nbytes for mats in weights.values() for m in mats)
+    names = dict((v, n) for n, v in SWEEP_TYPES)
+    avg = timed_grouped(lib, stream, sptr,
+                        [(f"{names[t]}_b{b}", t, lambda s, t=t, b=b: (descs[(t, b, (2 * s + BATCHES.index(b)) % COPIES)],
+                                                                     len(PROJECTIONS)), b) for t, b in launches],
+                        steps)
+    per = {}
+    for t, b in launches:
+        key = f"{names[t]}_b{b}"
+        nbytes = sum(m[0][3].nbytes for m in weights[t])
+        per[key] = {"avg_us": round(avg[key] * 1e6, 3), "bytes_per_launch": nbytes,
+                    "gbs": round(nbytes / avg[key] / 1e9, 1), "pct_hbm_peak": round(100 * nbytes / avg[key] / 8e12, 2)}
+    dom = max(per, key=lambda k: per[k]["avg_us"])
+    return {"workload": "Qwen3-0.6B decode projection type sweep: q 2048x1024, k/v 1024x1024, o 1024x2048, "
+                        "gate/up 3072x1024, down 1024x3072 x {Q4_0,Q5_1,Q8_0,Q3_K,Q5_K,Q6_K,IQ4_XS} x batch {1,8}, "
+                        f"one grouped launch per type and batch, {COPIES} weight copies",
+            "ms_per_sweep": round(dt * 1e3, 4), "gbs": round(bytes_per_set * len(BATCHES) / dt / 1e9, 1),
+            "per_launch": per,
+            "roofline": roofline_hbm(per[dom]["bytes_per_launch"], avg[dom], load_traffic("traffic_sweep", dom),
+                                     kernel=f"{launch_kernel_name(int(dom.rsplit('_b', 1)[1]))} {dom}", timing=TIMING)}
+
+
+def bench_lm_head(torch, np, quantize, lib, stream, sptr, device):
     """Qwen3 LM head: Q6_K 151936x1024, RMS-normalised N(0,1) input, logits + greedy id."""
     rows, cols = 151936, 1024
     p = quantized_normal(np, quantize, 14, rows * cols, SEED + 12)
@@ -359,12 +458,19 @@ def bench_lm_head(torch, np, quantize, stream, device):
     dt_head = time_graph(torch, stream, [lambda i=i: head(i) for i in range(reps)])
     dt_mv = time_graph(torch, stream, [lambda i=i: device.matvec(14, ws[i % 3], xs[i % 6], rows, cols, out=logits)
                                        for i in range(reps)])
+    arrs = [_descs(np, [(14, rows, cols, p)], xs[i % 6], [logits], [ws[i % 3]]) for i in range(6)]
+    avg = timed_grouped(lib, stream, sptr, [("head", 14, lambda s: (arrs[s % 6], 1), 1)], 24)["head"]
     return {"workload": "Q6_K 151936x1024 LM head, batch 1 (logits + exact greedy id)",
             "us_per_token": round(dt_head * 1e6, 2), "tokens_per_s": round(1 / dt_head, 1),
             "gbs": round(p.nbytes / dt_head / 1e9, 1),
             "pct_hbm_peak": round(100 * p.nbytes / dt_head / 1e9 / HBM_PEAK_GBS, 2),
             "matvec_only_us": round(dt_mv * 1e6, 2), "matvec_only_gbs": round(p.nbytes / dt_mv / 1e9, 1),
-            "bytes_per_token": p.nbytes}
+            "bytes_per_token": p.nbytes,
+            "roofline": roofline_hbm(p.nbytes, avg, load_traffic("traffic_configs", "lm_head_matvec"),
+                                     kernel="mv_kernel (VALU) Q6_K batch 1, the logits matvec", timing=TIMING),
+            "roofline_with_id": roofline_hbm(p.nbytes, dt_head, None,
+                                             kernel="bound matvec + lm_argmax_kernel per token",
+                                             timing="graph replay per token, both launches and the gap between")}
 
 
 def bench_moe(torch, np, quantize, stream, device, distinct_experts: int = 8):
@@ -401,68 +507,88 @@ def bench_moe(torch, np, quantize, stream, device, distinct_experts: int = 8):
         out[f"b{batch}"] = {"us_per_layer": round(dt * 1e6, 2), "tokens_per_s": round(batch / dt, 1),
                             "distinct_experts": round(float(np.mean(distinct)), 2),
                             "gbs": round(nbytes / dt / 1e9, 1),
-                            "pct_hbm_peak": round(100 * nbytes / dt / 1e9 / HBM_PEAK_GBS, 2)}
+                            "pct_hbm_peak": round(100 * nbytes / dt / 1e9 / HBM_PEAK_GBS, 2),
+                            "roofline": roofline_hbm(nbytes, dt, None,
+                                                     kernel="router, routing, gate/up, down and combine launches",
+                                                     timing="graph replay per layer call (all launches and the "
+                                                            "gaps between them); bytes = router + the distinct "
+                                                            "experts' gate/up/down slices")}
     out["workload"] = ("Qwen3-30B-A3B MoE FFN layer: router F32 2048x128, gate/up Q4_K [128x768x2048], "
                        f"down Q6_K [128x2048x768], top-8, renormalised; {distinct_experts} seeded quantized "
                        "experts tiled over the 128 slices, 2 layer copies alternated, distinct inputs per call")
     return out
 
 
-def bench_llama(torch, np, quantize, stream, device, lib, sptr):
-    """Llama-3-8B layer in Q4_K_M mix: decode (batch 1) and 512-token prefill."""
-    shapes = [("q", 12, 4096, 4096), ("k", 12, 1024, 4096), ("v", 12, 1024, 4096), ("o", 12, 4096, 4096),
-              ("gate", 12, 14336, 4096), ("up", 12, 14336, 4096), ("down", 14, 4096, 14336)]
-    cache = {}
-    mats = []
-    for name, t, rows, cols in shapes:
-        key = (t, rows, cols)
-        if key not in cache:
-            cache[key] = quantized_normal(np, quantize, t, rows * cols, SEED + 20 + len(cache))
-        mats.append((name, t, rows, cols, cache[key]))
-    layer_bytes = sum(m[4].nbytes for m in mats)
-    copies = 3
-    dev = [[torch.from_numpy(m[4]).cuda() for m in mats] for _ in range(copies)]
+def llama_step_descs(np, torch, mats, batch, copies):
+    """Desc arrays of the layer's four launches for each weight copy, and the inputs/outputs."""
+    xs = {"normed": torch.randn(batch, 4096, device="cuda"), "attn": torch.randn(batch, 4096, device="cuda"),
+          "normed2": torch.randn(batch, 4096, device="cuda"), "act": torch.randn(batch, 14336, device="cuda")}
+    ys = {name: torch.empty(batch, rows, device="cuda") for name, (t, rows, cols, p) in mats.items()}
+    arrs = {}
+    for key, t, names, xname in DECODE_LAUNCHES:
+        for c in range(len(copies)):
+            arrs[(key, c)] = _descs(np, [mats[n] for n in names], xs[xname], [ys[n] for n in names],
+                                    [copies[c][n] for n in names])
+    return arrs, xs, ys
+
+
+def run_llama_step(lib, sptr, arrs, batch, c):
+    for key, t, names, _ in DECODE_LAUNCHES:
+        rc = lib.pyrite_dev_matvec_grouped(t, arrs[(key, c)], len(names), batch, sptr)
+        if rc != 0:
+            raise RuntimeError(f"{key} launch failed: {rc} {lib.pyrite_hip_last_error()}")
+
+
+def bench_llama(torch, np, quantize, stream, device, lib, sptr, mats):
+    """Llama-3-8B layer in Q4_K_M mix: its q, gate and down matrices alone at batch 1,
+    and the 512-token prefill (four launches, MFMA dequant-GEMM)."""
+    layer_bytes = sum(p.nbytes for _, _, _, p in mats.values())
     res = {"workload": "Llama-3-8B layer, Q4_K_M mix: q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096 Q4_K, "
                        "down 4096x14336 Q6_K", "bytes_per_layer": layer_bytes}
-    for batch, reps in ((1, 12), (512, 2)):
-        xs = {c: torch.randn(batch, c, device="cuda") for c in (4096, 14336)}
-        ys = [torch.empty(batch, m[2], device="cuda") for m in mats]
-
-        def layer(i):
-            ws = dev[i % copies]
-            q4 = [j for j, m in enumerate(mats) if m[1] == 12]
-            arr = (Desc * len(q4))()
-            for a, j in enumerate(q4):
-                _, t, rows, cols, p = mats[j]
-                arr[a] = Desc(ws[j].data_ptr(), p.nbytes, rows, cols, xs[cols].data_ptr(), cols, ys[j].data_ptr(), rows)
-            rc = lib.pyrite_dev_matvec_grouped(12, arr, len(q4), batch, sptr)
-            if rc != 0:
-                raise RuntimeError(f"grouped matvec failed: {rc} {lib.pyrite_hip_last_error()}")
-            j = len(mats) - 1
-            device.matvec(14, ws[j], xs[14336], mats[j][2], mats[j][3], out=ys[j])
-        dt = time_graph(torch, stream, [lambda i=i: layer(i) for i in range(reps)])
-        flops = 2.0 * batch * sum(m[2] * m[3] for m in mats)
-        key = "decode_b1" if batch == 1 else "prefill_512"
-        res[key] = {"us": round(dt * 1e6, 2), "gbs": round(layer_bytes / dt / 1e9, 1),
-                    "pct_hbm_peak": round(100 * layer_bytes / dt / 1e9 / HBM_PEAK_GBS, 2),
-                    "tflops": round(flops / dt / 1e12, 2)}
-    del dev
+    # prefill: 2 weight copies, 2 steps per graph
+    copies = [{n: torch.from_numpy(m[3]).cuda() for n, m in mats.items()} for _ in range(2)]
+    batch = 512
+    arrs, xs, ys = llama_step_descs(np, torch, mats, batch, copies)
+    dt = time_graph(torch, stream, [lambda c=c: run_llama_step(lib, sptr, arrs, batch, c) for c in (0, 1)])
+    flops = 2.0 * batch * sum(r * c for _, r, c, _ in mats.values())
+    avg = timed_grouped(lib, stream, sptr, [(key, t, lambda s, key=key, names=names: (arrs[(key, s % 2)], len(names)),
+                                             batch) for key, t, names, _ in DECODE_LAUNCHES], 4)
+    per = {}
+    for key, t, names, _ in DECODE_LAUNCHES:
+        f = 2.0 * batch * sum(mats[n][1] * mats[n][2] for n in names)
+        per[key] = {"avg_us": round(avg[key] * 1e6, 2), "tflops": round(f / avg[key] / 1e12, 1),
+                    "frac_of_mfma_peak": round(f / avg[key] / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
+    dom = max(per, key=lambda k: avg[k])
+    fd = 2.0 * batch * sum(mats[n][1] * mats[n][2] for n in dict((k, nm) for k, _, nm, _ in DECODE_LAUNCHES)[dom])
+    res["prefill_512"] = {"us": round(dt * 1e6, 2), "tflops": round(flops / dt / 1e12, 2),
+                          "per_launch": per,
+                          "roofline": {"bound": "mfma", "achieved": round(fd / avg[dom] / 1e12, 1),
+                                       "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": round(fd / avg[dom] / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+                                       "traffic": None, "kernel": f"mg_kernel (MFMA dequant-GEMM) {dom} launch",
+                                       "flops_per_launch": fd, "avg_launch_us": round(avg[dom] * 1e6, 2),
+                                       "timing": TIMING}}
+    del copies, arrs, xs, ys
+    torch.cuda.empty_cache()
     # The layer's distinct matrix shapes alone at batch 1, each over rotated
     # copies of more than 600 MB (beyond the 256 MB Infinity Cache).
     singles = {}
-    for name, t, rows, cols, p in mats:
-        if name not in ("q", "gate", "down"):
-            continue
+    for name in ("q", "gate", "down"):
+        t, rows, cols, p = mats[name]
         n = max(2, int(np.ceil(600e6 / p.nbytes)))
         first = torch.from_numpy(p).cuda()
         ws1 = [first] + [first.clone() for _ in range(n - 1)]
         x1 = torch.randn(1, cols, device="cuda")
         y1 = torch.empty(1, rows, device="cuda")
         dt = time_graph(torch, stream, [lambda w=w: device.matvec(t, w, x1, rows, cols, out=y1) for w in ws1 * 2])
+        arrs1 = [_descs(np, [mats[name]], x1, [y1], [w]) for w in ws1]
+        avg1 = timed_grouped(lib, stream, sptr, [(name, t, lambda s: (arrs1[s % len(arrs1)], 1), 1)], 2 * n)[name]
         label = {12: "Q4_K", 14: "Q6_K"}[t]
         singles[f"{name} {rows}x{cols} {label}"] = {
             "us": round(dt * 1e6, 2), "gbs": round(p.nbytes / dt / 1e9, 1),
-            "pct_hbm_peak": round(100 * p.nbytes / dt / 1e9 / HBM_PEAK_GBS, 2)}
+            "pct_hbm_peak": round(100 * p.nbytes / dt / 1e9 / HBM_PEAK_GBS, 2),
+            "roofline": roofline_hbm(p.nbytes, avg1, load_traffic("traffic_llama_decode", name),
+                                     kernel=f"mv_kernel (VALU) {label} batch 1", timing=TIMING)}
         del ws1, first
     res["decode_b1_matrices"] = singles
     return res
@@ -475,11 +601,11 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-extra", action="store_true", help="skip the LM-head, MoE and Llama configurations")
+    ap.add_argument("--no-extra", action="store_true", help="skip the other workloads")
     ap.add_argument("--only", default=None,
-                    help="run only the named extra configuration (q4k_3072x1024, lm_head_q6k_151936x1024, "
-                         "moe_qwen3_30b_a3b, llama3_8b_layer, gguf_upload, copy_calibration) and print its JSON; "
-                         "for profiling")
+                    help="run only one workload and print its JSON, for profiling: llama_decode (the headline "
+                         "launches, eagerly), q4k_3072x1024, sweep, lm_head_q6k_151936x1024, moe_qwen3_30b_a3b, "
+                         "llama3_8b_layer, gguf_upload, copy_calibration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures the dequant-matvec path on one GPU; runs on more than one GPU "
@@ -489,70 +615,52 @@ def main() -> int:
     import numpy as np
     import torch
 
-    from pyrite_amd import _lib
+    from pyrite_amd import _lib, device
     from pyrite_amd.quantize import quantize
 
     lib = _lib.load()
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     torch.cuda.set_device(0)
-    if args.only:
-        from pyrite_amd import device
-        stream = torch.cuda.Stream()
-        torch.cuda.set_stream(stream)
-        sptr = ctypes.c_void_p(stream.cuda_stream)
-        fns = {"q4k_3072x1024": lambda: bench_q4k_single(torch, np, quantize, stream, device),
-               "lm_head_q6k_151936x1024": lambda: bench_lm_head(torch, np, quantize, stream, device),
-               "moe_qwen3_30b_a3b": lambda: bench_moe(torch, np, quantize, stream, device),
-               "llama3_8b_layer": lambda: bench_llama(torch, np, quantize, stream, device, lib, sptr),
-               "gguf_upload": lambda: bench_gguf_upload(torch, np),
-               "copy_calibration": lambda: copy_calibration(torch, stream)}
-        print(json.dumps({args.only: fns[args.only]()}), flush=True)
-        return 0
-    log("quantizing and uploading the sweep weights")
-    weights, bytes_per_set = build_weights(torch, np, quantize)
-    rng = np.random.default_rng(SEED + 1)
-    xs = {(cols, b): torch.from_numpy(rng.standard_normal((b, cols), dtype=np.float32)).cuda()
-          for cols in {c for _, _, c in PROJECTIONS} for b in BATCHES}
-    ys = {(t, i, b): torch.empty(b, rows, dtype=torch.float32, device="cuda")
-          for _, t in SWEEP_TYPES for i, (_, rows, _c) in enumerate(PROJECTIONS) for b in BATCHES}
-
-    descs = {}
-    for _, t in SWEEP_TYPES:
-        for b in BATCHES:
-            for c in range(COPIES):
-                arr = (Desc * len(PROJECTIONS))()
-                for i, (rows, cols, payload, copies) in enumerate(weights[t]):
-                    x = xs[(cols, b)]
-                    y = ys[(t, i, b)]
-                    arr[i] = Desc(copies[c].data_ptr(), payload.nbytes, rows, cols, x.data_ptr(), cols,
-                                  y.data_ptr(), rows)
-                descs[(t, b, c)] = arr
     # all work goes on one side stream (default priority): graphs cannot be
     # captured on the default stream
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
     torch.cuda.set_stream(stream)
     sptr = ctypes.c_void_p(stream.cuda_stream)
-    fn = lib.pyrite_dev_matvec_grouped
+    others = {
+        "q4k_3072x1024": lambda: bench_q4k_single(torch, np, quantize, lib, stream, sptr, device),
+        "sweep": lambda: bench_sweep(torch, np, quantize, lib, stream, sptr, 20),
+        "lm_head_q6k_151936x1024": lambda: bench_lm_head(torch, np, quantize, lib, stream, sptr, device),
+        "moe_qwen3_30b_a3b": lambda: bench_moe(torch, np, quantize, stream, device),
+        "llama3_8b_layer": lambda: bench_llama(torch, np, quantize, stream, device, lib, sptr,
+                                               llama_weights(np, quantize)),
+        "gguf_upload": lambda: bench_gguf_upload(torch, np),
+        "copy_calibration": lambda: copy_calibration(torch, stream),
+    }
+    if args.only and args.only != "llama_decode":
+        print(json.dumps({args.only: others[args.only]()}), flush=True)
+        return 0
 
-    launches = [(t, b) for b in BATCHES for _, t in SWEEP_TYPES]
+    log("quantizing and uploading the Llama-3-8B layer")
+    mats = llama_weights(np, quantize)
+    layer_bytes = sum(p.nbytes for _, _, _, p in mats.values())
+    copies = [{n: torch.from_numpy(m[3]).cuda() for n, m in mats.items()} for _ in range(DECODE_COPIES)]
+    arrs, xs, ys = llama_step_descs(np, torch, mats, 1, copies)
 
-    def step(s: int, events=None) -> None:
-        for k, (t, b) in enumerate(launches):
-            c = (2 * s + BATCHES.index(b)) % COPIES
-            if events is not None:
-                events[k][0].record(stream)
-            rc = fn(t, descs[(t, b, c)], len(PROJECTIONS), b, sptr)
-            if rc != 0:
-                raise RuntimeError(f"pyrite_dev_matvec_grouped({t}, batch {b}) returned {rc}: {_lib.last_error()}")
-            if events is not None:
-                events[k][1].record(stream)
+    def step(s: int) -> None:
+        run_llama_step(lib, sptr, arrs, 1, s % DECODE_COPIES)
 
-    bytes_per_step = bytes_per_set * len(BATCHES)
-    log(f"warmup {args.warmup} steps; {bytes_per_step / 1e6:.1f} MB of quantized weights per step")
+    log(f"warmup {args.warmup} steps; {layer_bytes / 1e6:.1f} MB of quantized weights per step")
     for s in range(args.warmup):
         step(s)
     torch.cuda.synchronize()
+    if args.only == "llama_decode":
+        for s in range(args.steps):
+            step(s)
+        torch.cuda.synchronize()
+        print(json.dumps({"llama_decode": {"steps": args.steps, "launches": [k for k, *_ in DECODE_LAUNCHES]}}),
+              flush=True)
+        return 0
     eager_out = {k: v.clone() for k, v in ys.items()}
 
     g = torch.cuda.CUDAGraph()
@@ -571,73 +679,51 @@ def main() -> int:
     g.replay()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    value = bytes_per_step * args.steps / elapsed / 1e9
+    value = layer_bytes * args.steps / elapsed / 1e9
 
-    # Per-kernel durations: the same launches again, eagerly, each timed by HIP
-    # events that the launch itself records at kernel start and end
-    # (pyrite_dev_matvec_grouped_timed -> hipExtLaunchKernelGGL), on this stream.
     log("per-kernel timing pass")
-    timed = lib.pyrite_dev_matvec_grouped_timed
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in launches]
-    for pair in evs:
-        for e in pair:
-            e.record(stream)  # creates the underlying hipEvent_t
-    torch.cuda.synchronize()
-    durations = {}
-    for s in range(args.steps):
-        for k, (t, b) in enumerate(launches):
-            c = (2 * s + BATCHES.index(b)) % COPIES
-            rc = timed(t, descs[(t, b, c)], len(PROJECTIONS), b, sptr, ctypes.c_void_p(evs[k][0].cuda_event),
-                       ctypes.c_void_p(evs[k][1].cuda_event))
-            if rc != 0:
-                raise RuntimeError(f"timed launch failed: {rc} {_lib.last_error()}")
-        torch.cuda.synchronize()
-        for k, key in enumerate(launches):
-            durations.setdefault(key, []).append(evs[k][0].elapsed_time(evs[k][1]) * 1e-3)
-    timing_source = ("HIP events recorded by each launch at kernel start/end (hipExtLaunchKernelGGL), "
-                     "same launches and weight rotation as the timed graph, on the same stream")
-
+    avg = timed_grouped(lib, stream, sptr,
+                        [(key, t, lambda s, key=key, names=names: (arrs[(key, s % DECODE_COPIES)], len(names)), 1)
+                         for key, t, names, _ in DECODE_LAUNCHES], args.steps)
     per_kernel = {}
-    for (t, b), ds in durations.items():
-        name = dict((v, n) for n, v in SWEEP_TYPES)[t]
-        nbytes = sum(p.nbytes for _, _, p, _ in weights[t])
-        avg = sum(ds) / len(ds)
-        per_kernel[f"{name}_b{b}"] = {"avg_us": avg * 1e6, "total_s": sum(ds), "bytes_per_launch": nbytes,
-                                      "gbs": nbytes / avg / 1e9}
-    dominant = max(per_kernel, key=lambda k: per_kernel[k]["total_s"])
-    dk = per_kernel[dominant]
-    dom_batch = int(dominant.rsplit("_b", 1)[1])
-    roofline = {"bound": "hbm", "achieved": round(dk["gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": load_traffic(dominant),
-                "kernel": f"{launch_kernel_name(dom_batch)} {dominant} (grouped launch over the 7 projections)",
-                "avg_launch_us": round(dk["avg_us"], 3), "bytes_per_launch": dk["bytes_per_launch"],
-                "timing": timing_source}
+    for key, t, names, _ in DECODE_LAUNCHES:
+        nbytes = sum(mats[n][3].nbytes for n in names)
+        per_kernel[key] = {"matrices": "+".join(names), "avg_us": round(avg[key] * 1e6, 3),
+                           "total_s": round(avg[key] * args.steps, 9), "bytes_per_launch": nbytes,
+                           "gbs": round(nbytes / avg[key] / 1e9, 1),
+                           "frac": round(nbytes / avg[key] / 1e9 / HBM_PEAK_GBS, 4)}
+    dom = max(per_kernel, key=lambda k: avg[k])
+    dnames = per_kernel[dom]["matrices"]
+    dtype = {12: "Q4_K", 14: "Q6_K"}[dict((k, t) for k, t, *_ in DECODE_LAUNCHES)[dom]]
+    roofline = roofline_hbm(per_kernel[dom]["bytes_per_launch"], avg[dom], load_traffic("traffic_llama_decode", dom),
+                            kernel=f"mv_kernel (VALU), the {dom} launch ({dnames}, {dtype}, batch 1)", timing=TIMING)
+    del g, copies, arrs, xs, ys
+    torch.cuda.empty_cache()
 
     extra = None
     if not args.no_extra:
-        from pyrite_amd import device
         extra = {}
-        for name, fn in (("q4k_3072x1024", lambda: bench_q4k_single(torch, np, quantize, stream, device)),
-                         ("lm_head_q6k_151936x1024", lambda: bench_lm_head(torch, np, quantize, stream, device)),
-                         ("moe_qwen3_30b_a3b", lambda: bench_moe(torch, np, quantize, stream, device)),
-                         ("llama3_8b_layer", lambda: bench_llama(torch, np, quantize, stream, device, lib,
-                                                                         sptr)),
-                         ("gguf_upload", lambda: bench_gguf_upload(torch, np))):
-            log(f"extra configuration: {name}")
-            extra[name] = fn()
+        for name in ("q4k_3072x1024", "sweep", "lm_head_q6k_151936x1024", "moe_qwen3_30b_a3b", "llama3_8b_layer",
+                     "gguf_upload"):
+            log(f"workload: {name}")
+            extra[name] = others[name]()
             torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu_baseline:
+        rng = np.random.default_rng(SEED + 7)
+        xv = {c: rng.standard_normal(c) for c in (4096, 14336)}
+        calls = [(t, p, xv[cols], rows, cols) for t, rows, cols, p in mats.values()]
+        what = "the Llama-3-8B layer decode (q, k, v, o, gate, up, down; one vector)"
         log(f"cpu baseline (~{args.cpu_seconds:.0f} s)")
-        cpu = run_cpu_baseline(weights, np, args.cpu_seconds)
+        cpu = run_cpu_baseline(calls, args.cpu_seconds, what)
         model, ncpu = cpu_info()
         cpu["host"] = f"{model}, {ncpu} logical CPUs visible"
-        # all host cores (at most 16, the box's CPU share)
-        nthreads = max(1, min(16, ncpu))
+        nthreads = max(1, min(16, ncpu))  # all host cores (at most 16, the box's CPU share)
         log(f"cpu baseline on {nthreads} threads (~{args.cpu_seconds:.0f} s)")
-        cpu["all_cores"] = run_cpu_baseline_parallel(weights, np, args.cpu_seconds, nthreads)
+        cpu["all_cores"] = run_cpu_baseline_parallel(calls, args.cpu_seconds, nthreads, what)
 
+    moe = (extra or {}).get("moe_qwen3_30b_a3b") or {}
     result = {
         "metric": "dequant-matvec GB/s on quantized bytes (% HBM peak); MoE-layer tokens/s at b=1/64",
         "value": round(value, 2),
@@ -652,18 +738,19 @@ def main() -> int:
         "dtype": "f32",
         "data": "synthetic: seeded N(0,0.02) fp32 weights quantized by pyrite_amd.quantize, N(0,1) fp32 activations",
         "config": {
-            "workload": "Qwen3-0.6B decode projection type sweep: q 2048x1024, k/v 1024x1024, o 1024x2048, "
-                        "gate/up 3072x1024, down 1024x3072 x {Q4_0,Q5_1,Q8_0,Q3_K,Q5_K,Q6_K,IQ4_XS} x batch {1,8}",
-            "bytes_per_step": bytes_per_step,
-            "weight_copies": COPIES,
-            "launches_per_step": len(launches),
+            "workload": "Llama-3-8B layer decode, batch 1, Q4_K_M mix: q/o 4096x4096, k/v 1024x4096, "
+                        "gate/up 14336x4096 Q4_K, down 4096x14336 Q6_K; four launches per step "
+                        "(q/k/v grouped, o, gate/up grouped, down)",
+            "bytes_per_step": layer_bytes,
+            "weight_copies": DECODE_COPIES,
+            "launches_per_step": len(DECODE_LAUNCHES),
         },
         "pct_hbm_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "roofline": roofline,
+        "moe_tokens_per_s": {b: moe[b]["tokens_per_s"] for b in ("b1", "b64") if b in moe} or None,
         "cpu_baseline": cpu,
+        "per_kernel": per_kernel,
         "workloads": extra,
-        "per_kernel": {k: {kk: round(vv, 3) if isinstance(vv, float) else vv for kk, vv in v.items()}
-                       for k, v in sorted(per_kernel.items())},
     }
     print(json.dumps(result), flush=True)
     return 0
