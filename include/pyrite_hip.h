@@ -172,6 +172,64 @@ int pyrite_dev_moe_ffn(const pyrite_moe_layer *layer, const float *x, size_t ldx
 int pyrite_dev_rms_norm(const float *x, size_t ldx, const float *weight, size_t n, double eps, float *y,
                         size_t ldy, size_t batch, void *stream);
 
+/* ------------------------------------------------------------ 3. layer operations */
+
+/* Residual add and RMSNorm in one pass: h_out[b] = h[b] + delta[b] (fp32), and
+ * normed[b] = rms_norm(h_out[b]) * weight (weight NULL = 1; fp64 inside, one
+ * rounding).  h_out may alias h.  Replaces the residual adds of
+ * pyrite/executor.py:795-811 (pyrite/dense.py:497-513) together with the
+ * rms_norm that follows each (the FFN norm, or the next layer's attention
+ * norm). */
+int pyrite_dev_add_rms_norm(const float *h, size_t ldh, const float *delta, size_t ldd, const float *weight,
+                            size_t n, double eps, float *h_out, size_t ldo, float *normed, size_t ldn,
+                            size_t batch, void *stream);
+
+/* The dense FFN's down projection with its activation fused in:
+ * y[b * ldy + r] = sum_c dequant(w)[r][c] * silu(gate[b * ldx + c]) * up[b * ldx + c],
+ * silu(v) = v / (1 + exp(-v)) for v > -60, else 0 (pyrite/tensor_ops.py:509-510),
+ * formed in fp32 while the matvec stages its input.  Block formats only (-1
+ * for plain types); gate and up 16-byte aligned, ldx % 4 == 0; the staged
+ * activations must fit 144 KiB of LDS, which holds at least 31040 columns
+ * per vector when one vector is staged and 15520 when two are (more for the
+ * 256-element formats), else -2.  Replaces the act and ffn_down steps of
+ * pyrite/dense.py:473-495. */
+int pyrite_dev_matvec_swiglu(int type_id, const void *w, size_t w_len, size_t rows, size_t cols,
+                             const float *gate, const float *up, size_t ldx, float *y, size_t ldy, size_t batch,
+                             void *stream);
+
+/* One layer's attention geometry and its KV cache (device fp32 arrays). */
+typedef struct pyrite_attention_layer {
+    size_t n_heads;        /* query heads (num_attention_heads) */
+    size_t n_kv_heads;     /* key/value heads; n_heads / n_kv_heads <= 16 */
+    size_t head_dim;       /* query/key width per head: even, <= 256 */
+    size_t value_dim;      /* value width per head: <= 256 */
+    size_t rotary_dim;     /* leading values of a head that RoPE rotates: even, <= head_dim; 0 = head_dim */
+    double rope_theta;
+    double eps;            /* RMSNorm epsilon of the QK-norm */
+    const float *q_norm;   /* [head_dim] QK-norm weights (attn_q_norm), or NULL: no query norm */
+    const float *k_norm;   /* [head_dim] (attn_k_norm), or NULL */
+    float *k_cache;        /* [capacity][n_kv_heads * head_dim], 8-byte aligned */
+    float *v_cache;        /* [capacity][n_kv_heads * value_dim] */
+    size_t capacity;       /* cache slots */
+} pyrite_attention_layer;
+
+/* Single-token attention (pyrite/executor.py:685-755 with _rope, :627-646):
+ * q [n_heads * head_dim], k [n_kv_heads * head_dim], v [n_kv_heads * value_dim]
+ * are this token's projections.  Each query and key head gets its QK-norm
+ * (when given) and NEOX RoPE at `position`; the key (rounded to fp32, as the
+ * reference's LayerKV stores it) and the value are written to cache slot
+ * `slot`; then every query head h attends, with scale 1 / sqrt(head_dim), to
+ * slots [0, n_ctx) of kv head h / (n_heads / n_kv_heads), and
+ * out [n_heads * value_dim] receives the softmax-weighted values.  Requires
+ * slot < n_ctx <= capacity.  The slots are a ring the caller manages: the
+ * reference's oldest-first eviction at max_kv_tokens (LayerKV.truncate,
+ * :130-134) is capacity = max_kv_tokens and slot = tokens seen % capacity
+ * (the attended set is the same; its order only changes fp rounding).
+ * Uses a per-device workspace grown on first use. */
+int pyrite_dev_attention_decode(const pyrite_attention_layer *layer, const float *q, const float *k,
+                                const float *v, size_t position, size_t slot, size_t n_ctx, float *out,
+                                void *stream);
+
 #ifdef __cplusplus
 }
 #endif

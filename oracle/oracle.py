@@ -136,6 +136,12 @@ class Oracle(_ABI):
             ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
             ctypes.c_int, ctypes.c_double, _dp, _dp, _ip, _dp, _dp)
         lib.oracle_moe_ffn.restype = ctypes.c_int
+        lib.oracle_rope.argtypes = (_dp, ctypes.c_size_t, ctypes.c_long, ctypes.c_double, ctypes.c_size_t)
+        lib.oracle_rope.restype = None
+        lib.oracle_attention.argtypes = (
+            _dp, _dp, _dp, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+            ctypes.c_double, ctypes.c_double, _dp, _dp, ctypes.c_long, _fp, _fp, ctypes.c_size_t, _dp)
+        lib.oracle_attention.restype = ctypes.c_int
 
     # -- inputs
     def normal(self, seed: int, n: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
@@ -189,6 +195,31 @@ class Oracle(_ABI):
     def argmax_first(self, v: np.ndarray) -> int:
         v = np.ascontiguousarray(v, dtype=np.float64)
         return int(self.lib.oracle_argmax_first(_ptr(v, _dp), v.size))
+
+    def rope(self, v: np.ndarray, position: int, theta: float, rotary_dim: int = 0) -> np.ndarray:
+        out = np.array(v, dtype=np.float64)
+        self.lib.oracle_rope(_ptr(out, _dp), out.size, position, theta, rotary_dim)
+        return out
+
+    def attention(self, q, k, v, n_heads, n_kv, head_dim, value_dim, k_cache, v_cache, n_prev, position,
+                  theta=10000.0, rotary_dim=0, eps=1e-6, q_norm=None, k_norm=None) -> np.ndarray:
+        """One token's attention; k_cache/v_cache (fp32, [n_prev + 1, ...]) receive its key and value."""
+        q = np.ascontiguousarray(q, dtype=np.float64)
+        k = np.ascontiguousarray(k, dtype=np.float64)
+        v = np.ascontiguousarray(v, dtype=np.float64)
+        assert k_cache.dtype == np.float32 and v_cache.dtype == np.float32
+        assert k_cache.flags.c_contiguous and v_cache.flags.c_contiguous
+        assert k_cache.size >= (n_prev + 1) * n_kv * head_dim and v_cache.size >= (n_prev + 1) * n_kv * value_dim
+        qn = None if q_norm is None else np.ascontiguousarray(q_norm, dtype=np.float64)
+        kn = None if k_norm is None else np.ascontiguousarray(k_norm, dtype=np.float64)
+        out = np.zeros(n_heads * value_dim, dtype=np.float64)
+        rc = self.lib.oracle_attention(_ptr(q, _dp), _ptr(k, _dp), _ptr(v, _dp), n_heads, n_kv, head_dim, value_dim,
+                                       rotary_dim, theta, eps, None if qn is None else _ptr(qn, _dp),
+                                       None if kn is None else _ptr(kn, _dp), position, _ptr(k_cache, _fp),
+                                       _ptr(v_cache, _fp), n_prev, _ptr(out, _dp))
+        if rc:
+            raise ValueError(f"oracle_attention error {rc}")
+        return out
 
     def route(self, logits: np.ndarray, k: int, norm_topk_prob: bool = True, scale: float = 1.0):
         lg = np.ascontiguousarray(logits, dtype=np.float64)

@@ -801,6 +801,68 @@ long oracle_argmax_first(const double *v, size_t n) {
     return (long)best;
 }
 
+void oracle_rope(double *v, size_t n, long position, double theta, size_t rotary_dim) {
+    /* pyrite/executor.py:627-646: pairs (i, i + half) of the first n_rot values */
+    size_t n_rot = rotary_dim == 0 ? n : (rotary_dim < n ? rotary_dim : n);
+    size_t half = n_rot / 2;
+    for (size_t i = 0; i < half; ++i) {
+        double freq = pow(theta, -2.0 * (double)i / (double)n_rot);
+        double angle = (double)position * freq;
+        double c = cos(angle), s = sin(angle);
+        double x0 = v[i], x1 = v[i + half];
+        v[i] = x0 * c - x1 * s;
+        v[i + half] = x0 * s + x1 * c;
+    }
+}
+
+int oracle_attention(const double *q, const double *k, const double *v, size_t n_heads, size_t n_kv,
+                     size_t head_dim, size_t value_dim, size_t rotary_dim, double theta, double eps,
+                     const double *q_norm, const double *k_norm, long position, float *k_cache,
+                     float *v_cache, size_t n_prev, double *out) {
+    /* pyrite/executor.py:685-755 (prep_head :712-715, cache append :729-733,
+     * scores, softmax and weighted values :739-754) */
+    if (n_heads == 0 || n_kv == 0 || n_heads % n_kv || head_dim == 0 || head_dim > 4096 || value_dim == 0)
+        return -2;
+    size_t group = n_heads / n_kv, n_tok = n_prev + 1;
+    double *qh = malloc(sizeof(double) * (head_dim * 2 + n_tok * 2));
+    if (!qh) return -3;
+    double *tmp = qh + head_dim, *scores = tmp + head_dim, *probs = scores + n_tok;
+    /* keys and values of this token: normed and rotated keys, stored as fp32 */
+    for (size_t g = 0; g < n_kv; ++g) {
+        const double *src = k + g * head_dim;
+        if (k_norm) oracle_rms_norm(src, k_norm, head_dim, eps, tmp);
+        else memcpy(tmp, src, sizeof(double) * head_dim);
+        oracle_rope(tmp, head_dim, position, theta, rotary_dim);
+        for (size_t i = 0; i < head_dim; ++i) k_cache[n_prev * n_kv * head_dim + g * head_dim + i] = (float)tmp[i];
+        for (size_t i = 0; i < value_dim; ++i)
+            v_cache[n_prev * n_kv * value_dim + g * value_dim + i] = (float)v[g * value_dim + i];
+    }
+    double scale = 1.0 / sqrt((double)head_dim);
+    for (size_t h = 0; h < n_heads; ++h) {
+        const double *src = q + h * head_dim;
+        if (q_norm) oracle_rms_norm(src, q_norm, head_dim, eps, qh);
+        else memcpy(qh, src, sizeof(double) * head_dim);
+        oracle_rope(qh, head_dim, position, theta, rotary_dim);
+        size_t g = h / group;
+        for (size_t t = 0; t < n_tok; ++t) {
+            const float *key = k_cache + t * n_kv * head_dim + g * head_dim;
+            double sc = 0.0;
+            for (size_t i = 0; i < head_dim; ++i) sc += qh[i] * (double)key[i];
+            scores[t] = sc * scale;
+        }
+        oracle_softmax(scores, n_tok, probs);
+        double *o = out + h * value_dim;
+        for (size_t i = 0; i < value_dim; ++i) o[i] = 0.0;
+        for (size_t t = 0; t < n_tok; ++t) {
+            if (probs[t] == 0.0) continue;
+            const float *val = v_cache + t * n_kv * value_dim + g * value_dim;
+            for (size_t i = 0; i < value_dim; ++i) o[i] += probs[t] * (double)val[i];
+        }
+    }
+    free(qh);
+    return 0;
+}
+
 int oracle_route(const double *logits, size_t n, size_t k, int norm_topk_prob,
                  double scale, int *ids, double *weights, double *probs_out) {
     /* pyrite/executor.py:765-774: softmax, order by (-p, e), keep k,

@@ -57,6 +57,20 @@ void oracle_softmax(const double *v, size_t n, double *out);
 double oracle_silu(double v);
 void oracle_rms_norm(const double *x, const double *w, size_t n, double eps, double *out);
 long oracle_argmax_first(const double *v, size_t n);
+/* pyrite/executor.py:627-646: NEOX RoPE of one head in place (the first
+ * rotary_dim values; 0 = all n) */
+void oracle_rope(double *v, size_t n, long position, double theta, size_t rotary_dim);
+/* pyrite/executor.py:685-755 after the q/k/v projections, for one token:
+ * per-head QK-norm (q_norm / k_norm may be NULL) and RoPE, the key and value
+ * appended to an fp32 cache at index n_prev (caches hold n_prev earlier
+ * tokens, oldest first: [n_prev + 1][n_kv * head_dim] and
+ * [n_prev + 1][n_kv * value_dim]), then every head's softmax-weighted values
+ * over all n_prev + 1 tokens into out [n_heads * value_dim].  -2 on a bad
+ * shape. */
+int oracle_attention(const double *q, const double *k, const double *v, size_t n_heads, size_t n_kv,
+                     size_t head_dim, size_t value_dim, size_t rotary_dim, double theta, double eps,
+                     const double *q_norm, const double *k_norm, long position, float *k_cache,
+                     float *v_cache, size_t n_prev, double *out);
 /* top-k routing: ids[k], weights[k]; probs[n] optional (may be NULL) */
 int oracle_route(const double *logits, size_t n_experts, size_t k, int norm_topk_prob,
                  double expert_weights_scale, int *ids, double *weights, double *probs);

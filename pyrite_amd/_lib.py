@@ -31,6 +31,10 @@ SIGNATURES: list[tuple[str, object, tuple]] = [
      (_c.c_int, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _sz, _vp, _sz, _vp)),
     ("pyrite_dev_moe_ffn", _c.c_int, (_vp, _vp, _sz, _vp, _sz, _vp, _vp, _sz, _vp)),
     ("pyrite_dev_rms_norm", _c.c_int, (_vp, _sz, _vp, _sz, _c.c_double, _vp, _sz, _sz, _vp)),
+    ("pyrite_dev_add_rms_norm", _c.c_int,
+     (_vp, _sz, _vp, _sz, _vp, _sz, _c.c_double, _vp, _sz, _vp, _sz, _sz, _vp)),
+    ("pyrite_dev_matvec_swiglu", _c.c_int, (_c.c_int, _vp, _sz, _sz, _sz, _vp, _vp, _sz, _vp, _sz, _sz, _vp)),
+    ("pyrite_dev_attention_decode", _c.c_int, (_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp, _vp)),
 ]
 
 _LIB: ctypes.CDLL | None = None

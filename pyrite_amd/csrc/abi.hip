@@ -238,6 +238,41 @@ int pyrite_dev_moe_ffn(const pyrite_moe_layer* layer, const float* x, size_t ldx
     return rc;
 }
 
+int pyrite_dev_add_rms_norm(const float* h, size_t ldh, const float* delta, size_t ldd, const float* weight,
+                            size_t n, double eps, float* h_out, size_t ldo, float* normed, size_t ldn, size_t batch,
+                            void* stream) {
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;
+    const int rc = add_rms_norm_launch(h, ldh, delta, ldd, weight, n, eps, h_out, ldo, normed, ldn, batch, s);
+    if (rc == -4) return fail(-4, "pyrite_dev_add_rms_norm: launch", hipGetLastError());
+    return rc;
+}
+
+int pyrite_dev_matvec_swiglu(int type_id, const void* w, size_t w_len, size_t rows, size_t cols, const float* gate,
+                             const float* up, size_t ldx, float* y, size_t ldy, size_t batch, void* stream) {
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;
+    const int rc = matvec_swiglu_launch(type_id, static_cast<const uint8_t*>(w), w_len, rows, cols, gate, up, ldx, y,
+                                        ldy, batch, s);
+    if (rc == -4) return fail(-4, "pyrite_dev_matvec_swiglu: launch", hipGetLastError());
+    return rc;
+}
+
+int pyrite_dev_attention_decode(const pyrite_attention_layer* layer, const float* q, const float* k,
+                                const float* v, size_t position, size_t slot, size_t n_ctx, float* out,
+                                void* stream) {
+    if (!layer) return -3;
+    static_assert(sizeof(pyrite_attention_layer) == sizeof(AttnLayer), "attention layer layout");
+    hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;
+    AttnLayer L;
+    memcpy(&L, layer, sizeof L);
+    if (L.rotary_dim == 0) L.rotary_dim = L.head_dim;  // the reference's `rotary_dim or head_dim`
+    const int rc = attention_decode_launch(L, q, k, v, position, slot, n_ctx, out, s);
+    if (rc != 0) {
+        if (const char* m = attn_last_error()) return fail(rc, m);
+        if (rc == -4) return fail(-4, "pyrite_dev_attention_decode: launch", hipGetLastError());
+    }
+    return rc;
+}
+
 int pyrite_dev_rms_norm(const float* x, size_t ldx, const float* weight, size_t n, double eps, float* y, size_t ldy,
                         size_t batch, void* stream) {
     hipStream_t s = stream ? static_cast<hipStream_t>(stream) : hipStreamPerThread;

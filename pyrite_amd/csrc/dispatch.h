@@ -124,6 +124,32 @@ const char* moe_last_error();
 int rms_norm_launch(const float* X, size_t ldx, const float* Wt, size_t n, double eps, float* Y, size_t ldy,
                     size_t batch, hipStream_t stream);
 
+// layer.hip: residual add + RMSNorm (Hout may alias H), the SwiGLU-staged
+// down projection, and single-token attention over an fp32 KV cache.
+int add_rms_norm_launch(const float* H, size_t ldh, const float* D, size_t ldd, const float* Wt, size_t n,
+                        double eps, float* Hout, size_t ldo, float* N, size_t ldn, size_t batch,
+                        hipStream_t stream);
+int matvec_swiglu_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t cols, const float* G,
+                         const float* U, size_t ldx, float* Y, size_t ldy, size_t batch, hipStream_t stream);
+// layout identical to pyrite_attention_layer of include/pyrite_hip.h
+struct AttnLayer {
+    size_t n_heads;
+    size_t n_kv_heads;
+    size_t head_dim;
+    size_t value_dim;
+    size_t rotary_dim;
+    double rope_theta;
+    double eps;
+    const float* q_norm;
+    const float* k_norm;
+    float* k_cache;
+    float* v_cache;
+    size_t capacity;
+};
+int attention_decode_launch(const AttnLayer& L, const float* q, const float* k, const float* v, size_t position,
+                            size_t slot, size_t n_ctx, float* out, hipStream_t stream);
+const char* attn_last_error();
+
 // abi.hip: grow a per-device workspace block to at least `want` bytes
 // (geometrically: at least twice the old capacity), zero-filled when `zero`.
 // The replaced block is never freed: a HIP graph captured before the growth

@@ -341,12 +341,14 @@ __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* sm
 // NW waves per workgroup: 4, or 8-16 for launches whose staged activations
 // would otherwise limit the workgroups per CU (long rows): then one copy of x
 // in LDS serves 8-16 waves.
-template <int T, int B, int R, bool AL, bool XL, bool BD, int NW = kMvWaves>
+// XS: how activations are fetched while staged (XDirect; XSwiglu stages
+// silu(gate) * up for a down projection, which needs XL).
+template <int T, int B, int R, bool AL, bool XL, bool BD, int NW = kMvWaves, class XS = XDirect>
 __global__ __launch_bounds__(64 * NW) void mv_kernel(const MvGroup g) {
     extern __shared__ float smem[];
     int i = 0;
     while (i + 1 < g.n && (int)blockIdx.x >= g.d[i + 1].wg_begin) ++i;
-    mv_body<T, B, R, AL, XL, BD, XDirect, NW>(g.d[i], (long long)blockIdx.x - g.d[i].wg_begin, smem);
+    mv_body<T, B, R, AL, XL, BD, XS, NW>(g.d[i], (long long)blockIdx.x - g.d[i].wg_begin, smem);
 }
 
 // ---------------------------------------------------------------- launcher
@@ -387,11 +389,11 @@ static const DevInfo& dev_info() {
 }
 
 // Workgroups of one kernel instance resident per CU, from its register use.
-template <int T, int B, int R, bool AL, bool XL, bool BD, int NW = kMvWaves>
+template <int T, int B, int R, bool AL, bool XL, bool BD, int NW = kMvWaves, class XS = XDirect>
 static int wgs_per_cu_regs() {
     static const int n = [] {
         int v = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, mv_kernel<T, B, R, AL, XL, BD, NW>, 64 * NW, 0) !=
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, mv_kernel<T, B, R, AL, XL, BD, NW, XS>, 64 * NW, 0) !=
                 hipSuccess ||
             v < 1)
             v = 1;
@@ -431,10 +433,10 @@ static int plan_lpr(long long U) {
     return log2_ceil(per_lane < 64 ? per_lane : 64);
 }
 
-template <int T, int B, int R, bool AL, bool XL, bool BD, int NW = kMvWaves>
+template <int T, int B, int R, bool AL, bool XL, bool BD, int NW = kMvWaves, class XS = XDirect>
 static long long resident_wgs(size_t lds) {
     const DevInfo& di = dev_info();
-    long long per_cu = wgs_per_cu_regs<T, B, R, AL, XL, BD, NW>();
+    long long per_cu = wgs_per_cu_regs<T, B, R, AL, XL, BD, NW, XS>();
     if (lds > 0 && (long long)(di.lds_per_cu / lds) < per_cu) per_cu = (long long)(di.lds_per_cu / lds);
     if (per_cu < 1) per_cu = 1;
     return per_cu * di.cus;
@@ -511,66 +513,82 @@ struct LaunchEvents {
     hipEvent_t stop = nullptr;
 };
 
-template <int T, int B, int R, bool AL, bool XL, bool BD, int NW>
+template <int T, int B, int R, bool AL, bool XL, bool BD, int NW, class XS = XDirect>
 static hipError_t launch_group_w(MvGroup g, size_t lds, hipStream_t stream, LaunchEvents ev) {
     if (lds > 65536) {
         static const hipError_t attr =
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&mv_kernel<T, B, R, AL, XL, BD, NW>),
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&mv_kernel<T, B, R, AL, XL, BD, NW, XS>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, kMvXlMax);
         if (attr != hipSuccess) return attr;
     }
-    const long long wgs = plan_group(g, R, resident_wgs<T, B, R, AL, XL, BD, NW>(lds), NW);
+    const long long wgs = plan_group(g, R, resident_wgs<T, B, R, AL, XL, BD, NW, XS>(lds), NW);
     if (wgs <= 0 || wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
     if (ev.start || ev.stop)
-        hipExtLaunchKernelGGL((mv_kernel<T, B, R, AL, XL, BD, NW>), dim3((unsigned)wgs), dim3(64 * NW), (uint32_t)lds,
-                              stream, ev.start, ev.stop, 0, g);
+        hipExtLaunchKernelGGL((mv_kernel<T, B, R, AL, XL, BD, NW, XS>), dim3((unsigned)wgs), dim3(64 * NW),
+                              (uint32_t)lds, stream, ev.start, ev.stop, 0, g);
     else
-        hipLaunchKernelGGL((mv_kernel<T, B, R, AL, XL, BD, NW>), dim3((unsigned)wgs), dim3(64 * NW), lds, stream, g);
+        hipLaunchKernelGGL((mv_kernel<T, B, R, AL, XL, BD, NW, XS>), dim3((unsigned)wgs), dim3(64 * NW), lds, stream,
+                           g);
     return hipGetLastError();
 }
 
 // Staged activations that hold a CU below the workgroups its registers allow
 // (long rows) switch batch-1 launches to 16-wave workgroups and batch-2
 // launches to 8-wave ones (16 waves would cap them at 128 VGPRs and spill).
-template <int T, int B, int R, bool AL, bool XL, bool BD>
+template <int T, int B, int R, bool AL, bool XL, bool BD, class XS = XDirect>
 static hipError_t launch_group_r(MvGroup g, size_t lds, hipStream_t stream, LaunchEvents ev) {
     if constexpr (XL && B <= 2 && !BD) {
         constexpr int NW = B == 1 ? 16 : 8;
         const DevInfo& di = dev_info();
-        const long long by_regs = wgs_per_cu_regs<T, B, R, AL, XL, BD>();
+        const long long by_regs = wgs_per_cu_regs<T, B, R, AL, XL, BD, kMvWaves, XS>();
         if (lds > 0 && (long long)(di.lds_per_cu / lds) < by_regs && lds <= di.lds_per_cu &&
-            matvec_waves_env() != 4 && wgs_per_cu_regs<T, B, R, AL, XL, BD, NW>() >= 1)
-            return launch_group_w<T, B, R, AL, XL, BD, NW>(g, lds, stream, ev);
+            matvec_waves_env() != 4 && wgs_per_cu_regs<T, B, R, AL, XL, BD, NW, XS>() >= 1)
+            return launch_group_w<T, B, R, AL, XL, BD, NW, XS>(g, lds, stream, ev);
     }
-    return launch_group_w<T, B, R, AL, XL, BD, kMvWaves>(g, lds, stream, ev);
+    return launch_group_w<T, B, R, AL, XL, BD, kMvWaves, XS>(g, lds, stream, ev);
 }
 
-template <int T, int B, int R, bool AL, bool BD>
+template <int T, int B, int R, bool AL, bool BD, class XS = XDirect>
 static hipError_t launch_group_rx(const MvGroup& g, hipStream_t stream, LaunchEvents ev) {
     int max_cols = 0;
     for (int i = 0; i < g.n; ++i) max_cols = g.d[i].cols > max_cols ? g.d[i].cols : max_cols;
     if constexpr (Geo<T>::bs > 1) {
         if (use_xl_mv<T, B, BD>(max_cols))
-            return launch_group_r<T, B, R, AL, true, BD>(g, lds_bytes<T, B, BD>(max_cols, true), stream, ev);
+            return launch_group_r<T, B, R, AL, true, BD, XS>(g, lds_bytes<T, B, BD>(max_cols, true), stream, ev);
     }
-    return launch_group_r<T, B, R, AL, false, BD>(g, lds_bytes<T, B, BD>(max_cols, false), stream, ev);
+    if constexpr (std::is_same<XS, XDirect>::value)
+        return launch_group_r<T, B, R, AL, false, BD>(g, lds_bytes<T, B, BD>(max_cols, false), stream, ev);
+    else
+        return hipErrorInvalidValue;  // indirect activations are only staged
 }
 
-template <int T, int B, bool AL, bool BD>
+template <int T, int B, bool AL, bool BD, class XS = XDirect>
 static hipError_t launch_group(const MvGroup& g, hipStream_t stream, LaunchEvents ev) {
     MvGroup sg = g;
     for (int i = 0; i < sg.n; ++i) sg.d[i].lpr_log2 = mat_shape<T, B, AL>(sg.d[i].rows, sg.d[i].cols).lpr_log2;
-    return launch_group_rx<T, B, 1, AL, BD>(sg, stream, ev);
+    return launch_group_rx<T, B, 1, AL, BD, XS>(sg, stream, ev);
 }
 
-template <int T, bool AL, bool BD>
+// Batch chunks 1, 2, 4 and 8; the SwiGLU-staged down projection (XSwiglu)
+// exists for chunks of 1 and 2 and the block formats.
+template <int T, bool AL, bool BD, class XS = XDirect>
 static hipError_t launch_type(int batch, const MvGroup& g, hipStream_t s, LaunchEvents ev) {
-    switch (batch) {
-    case 1: return launch_group<T, 1, AL, BD>(g, s, ev);
-    case 2: return launch_group<T, 2, AL, BD>(g, s, ev);
-    case 4: return launch_group<T, 4, AL, BD>(g, s, ev);
-    case 8: return launch_group<T, 8, AL, BD>(g, s, ev);
-    default: return hipErrorInvalidValue;
+    if constexpr (std::is_same<XS, XDirect>::value) {
+        switch (batch) {
+        case 1: return launch_group<T, 1, AL, BD>(g, s, ev);
+        case 2: return launch_group<T, 2, AL, BD>(g, s, ev);
+        case 4: return launch_group<T, 4, AL, BD>(g, s, ev);
+        case 8: return launch_group<T, 8, AL, BD>(g, s, ev);
+        default: return hipErrorInvalidValue;
+        }
+    } else if constexpr (Geo<T>::bs > 1 && !BD) {
+        switch (batch) {
+        case 1: return launch_group<T, 1, AL, BD, XS>(g, s, ev);
+        case 2: return launch_group<T, 2, AL, BD, XS>(g, s, ev);
+        default: return hipErrorInvalidValue;
+        }
+    } else {
+        return hipErrorInvalidValue;
     }
 }
 
@@ -614,16 +632,31 @@ static int valu_chunk(int type, size_t left, size_t max_cols) {
 #undef PYRITE_CASE
 }
 
+// Whether a chunk of c (1 or 2) vectors of max_cols columns stages its
+// activations in LDS (the SwiGLU-staged matvec requires it).
+static bool valu_staged(int type, int c, size_t max_cols) {
+#define PYRITE_CASE(T) \
+    case T: return c == 1 ? use_xl_mv<T, 1, false>((int)max_cols) : use_xl_mv<T, 2, false>((int)max_cols);
+    switch (type) {
+        PYRITE_FOR_EACH_TYPE(PYRITE_CASE)
+    default: return false;
+    }
+#undef PYRITE_CASE
+}
+
 // VALU launches over batch chunks and groups of kMaxGroup matrices; bnd
 // (BD only) holds one bound buffer per matrix, laid out like its y.
-template <bool BD>
+// XSwiglu: mats[i].x holds the gate rows and up[i] the up rows (same ldx);
+// chunks are at most 2 vectors and must stage their activations in LDS.
+template <bool BD, class XS = XDirect>
 static int valu_group_launch(int type, const TypeGeo& g, bool al, const MatvecArgs* mats, float* const* bnd,
                              size_t n, size_t batch, size_t max_cols, hipStream_t stream, hipEvent_t start,
-                             hipEvent_t stop) {
+                             hipEvent_t stop, const float* const* up = nullptr) {
+    constexpr bool kSwiglu = !std::is_same<XS, XDirect>::value;
     size_t done = 0;
     while (done < batch) {
-        const int c = valu_chunk<BD>(type, batch - done, max_cols);
-        if (c == 0) return -2;
+        const int c = valu_chunk<BD>(type, kSwiglu && batch - done > 2 ? 2 : batch - done, max_cols);
+        if (c == 0 || (kSwiglu && (c > 2 || !valu_staged(type, c, max_cols)))) return -2;
         for (size_t base = 0; base < n; base += kMaxGroup) {
             LaunchEvents ev;
             if (done == 0 && base == 0) ev.start = start;
@@ -643,12 +676,13 @@ static int valu_group_launch(int type, const TypeGeo& g, bool al, const MatvecAr
                 dd.cols = (int)m.cols;
                 dd.pad = 0;
                 dd.Bnd = BD ? bnd[base + i] + done * m.ldy : nullptr;
+                dd.X2 = kSwiglu ? up[base + i] + done * m.ldx : nullptr;
             }
             hipError_t e = hipSuccess;
 #define PYRITE_CASE(T)                                                                       \
     case T:                                                                                \
-        e = al ? launch_type<T, (Geo<T>::bpb % 4 == 0), BD>(c, grp, stream, ev)            \
-               : launch_type<T, false, BD>(c, grp, stream, ev);                            \
+        e = al ? launch_type<T, (Geo<T>::bpb % 4 == 0), BD, XS>(c, grp, stream, ev)        \
+               : launch_type<T, false, BD, XS>(c, grp, stream, ev);                        \
         break;
             switch (type) {
                 PYRITE_FOR_EACH_TYPE(PYRITE_CASE)

@@ -248,3 +248,120 @@ def moe_ffn(layer: MoeLayer, x: torch.Tensor, out: torch.Tensor | None = None
                                   ids.data_ptr(), wts.data_ptr(), batch, _stream_ptr(dev))
     _lib.check(code, "pyrite_dev_moe_ffn")
     return out, ids, wts
+
+
+def add_rms_norm(h: torch.Tensor, delta: torch.Tensor, weight: torch.Tensor | None, eps: float,
+                 h_out: torch.Tensor | None = None, normed: torch.Tensor | None = None
+                 ) -> tuple[torch.Tensor, torch.Tensor]:
+    """Residual add and RMSNorm in one launch: h_out = h + delta (fp32) and
+    normed = rms_norm(h_out) * weight (pyrite/executor.py:795-811).  h_out may be h."""
+    n = h.shape[-1]
+    h2 = _activations(h, h.device, n, "h")
+    d2 = _activations(delta, h.device, n, "delta")
+    batch = h2.shape[0]
+    if d2.shape[0] != batch:
+        raise ValueError("h and delta need the same number of vectors")
+    if weight is not None and (weight.dtype != torch.float32 or weight.numel() != n or not weight.is_contiguous()
+                               or weight.device != h.device):
+        raise ValueError("weight must be a contiguous fp32 tensor of h's last dim on h's device")
+    h_out = torch.empty_like(h2) if h_out is None else h_out
+    normed = torch.empty_like(h2) if normed is None else normed
+    o2 = _output(h_out, h.device, batch, n, "h_out")
+    n2 = _output(normed, h.device, batch, n, "normed")
+    lib = _lib.load()
+    code = lib.pyrite_dev_add_rms_norm(h2.data_ptr(), _ld(h2), d2.data_ptr(), _ld(d2),
+                                       weight.data_ptr() if weight is not None else None, n, float(eps),
+                                       o2.data_ptr(), _ld(o2), n2.data_ptr(), _ld(n2), batch, _stream_ptr(h.device))
+    _lib.check(code, "pyrite_dev_add_rms_norm")
+    return h_out, normed
+
+
+def matvec_swiglu(type_id: int, w: torch.Tensor, gate: torch.Tensor, up: torch.Tensor, rows: int, cols: int,
+                  out: torch.Tensor | None = None) -> torch.Tensor:
+    """y[b] = dequant(w) @ (silu(gate[b]) * up[b]): the dense FFN's down projection with its
+    activation formed while the input is staged (pyrite/dense.py:473-495)."""
+    _check_weights(type_id, w, rows, cols)
+    squeeze = gate.dim() == 1
+    g2 = _activations(gate, w.device, cols, "gate")
+    u2 = _activations(up, w.device, cols, "up")
+    if u2.shape != g2.shape or _ld(u2) != _ld(g2):
+        raise ValueError("gate and up need the same shape and row stride")
+    batch = g2.shape[0]
+    if out is None:
+        out = torch.empty(batch, rows, dtype=torch.float32, device=w.device)
+    y2 = _output(out, w.device, batch, rows)
+    lib = _lib.load()
+    code = lib.pyrite_dev_matvec_swiglu(type_id, w.data_ptr(), w.numel(), rows, cols, g2.data_ptr(), u2.data_ptr(),
+                                        _ld(g2), y2.data_ptr(), _ld(y2), batch, _stream_ptr(w.device))
+    _lib.check(code, "pyrite_dev_matvec_swiglu")
+    return out.reshape(rows) if squeeze else out
+
+
+class _AttnLayerC(ctypes.Structure):
+    """pyrite_attention_layer (include/pyrite_hip.h)."""
+    _fields_ = [("n_heads", ctypes.c_size_t), ("n_kv_heads", ctypes.c_size_t), ("head_dim", ctypes.c_size_t),
+                ("value_dim", ctypes.c_size_t), ("rotary_dim", ctypes.c_size_t), ("rope_theta", ctypes.c_double),
+                ("eps", ctypes.c_double), ("q_norm", ctypes.c_void_p), ("k_norm", ctypes.c_void_p),
+                ("k_cache", ctypes.c_void_p), ("v_cache", ctypes.c_void_p), ("capacity", ctypes.c_size_t)]
+
+
+@dataclass
+class AttentionCache:
+    """One layer's attention geometry and its fp32 KV cache in device memory
+    (the reference's LayerKV, pyrite/executor.py:79-141, as a ring of
+    ``capacity`` slots; capacity = max_kv_tokens keeps the oldest-first
+    eviction of LayerKV.truncate)."""
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    value_dim: int
+    capacity: int
+    rope_theta: float = 10000.0
+    rotary_dim: int = 0
+    eps: float = 1e-6
+    q_norm: torch.Tensor | None = None
+    k_norm: torch.Tensor | None = None
+    device: str | torch.device = "cuda"
+    tokens: int = 0  # tokens appended so far
+
+    def __post_init__(self):
+        self.k_cache = torch.zeros(self.capacity, self.n_kv_heads * self.head_dim, device=self.device)
+        self.v_cache = torch.zeros(self.capacity, self.n_kv_heads * self.value_dim, device=self.device)
+        for t in (self.q_norm, self.k_norm):
+            if t is not None and (t.dtype != torch.float32 or t.numel() != self.head_dim or not t.is_contiguous()
+                                  or t.device != self.k_cache.device):
+                raise ValueError("QK-norm weights must be contiguous fp32 [head_dim] on the cache's device")
+
+    def _c(self) -> _AttnLayerC:
+        return _AttnLayerC(self.n_heads, self.n_kv_heads, self.head_dim, self.value_dim, self.rotary_dim,
+                           float(self.rope_theta), float(self.eps),
+                           self.q_norm.data_ptr() if self.q_norm is not None else None,
+                           self.k_norm.data_ptr() if self.k_norm is not None else None,
+                           self.k_cache.data_ptr(), self.v_cache.data_ptr(), self.capacity)
+
+
+def attention_decode(cache: AttentionCache, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, position: int,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """One token's attention (pyrite/executor.py:685-755): QK-norm and RoPE at
+    ``position``, the key and value appended to the cache, softmax-weighted values of
+    every head over the cached tokens.  Returns [n_heads * value_dim] fp32."""
+    dev = cache.k_cache.device
+    nq, nk, nv = cache.n_heads * cache.head_dim, cache.n_kv_heads * cache.head_dim, cache.n_kv_heads * cache.value_dim
+    for name, t, n in (("q", q, nq), ("k", k, nk), ("v", v, nv)):
+        if (not isinstance(t, torch.Tensor) or not t.is_cuda or t.device != dev or t.dtype != torch.float32
+                or t.numel() != n or not t.is_contiguous()):
+            raise ValueError(f"{name} must be a contiguous fp32 tensor of {n} values on {dev}")
+    if out is None:
+        out = torch.empty(cache.n_heads * cache.value_dim, dtype=torch.float32, device=dev)
+    elif (out.dtype != torch.float32 or out.device != dev or out.numel() != cache.n_heads * cache.value_dim
+          or not out.is_contiguous()):
+        raise ValueError("out must be a contiguous fp32 tensor of n_heads * value_dim values")
+    slot = cache.tokens % cache.capacity
+    n_ctx = min(cache.tokens + 1, cache.capacity)
+    c = cache._c()
+    lib = _lib.load()
+    code = lib.pyrite_dev_attention_decode(ctypes.addressof(c), q.data_ptr(), k.data_ptr(), v.data_ptr(), position,
+                                           slot, n_ctx, out.data_ptr(), _stream_ptr(dev))
+    _lib.check(code, "pyrite_dev_attention_decode")
+    cache.tokens += 1
+    return out
