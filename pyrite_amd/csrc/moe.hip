@@ -12,6 +12,8 @@
 //
 // Kernels, all on one stream, no host round trip:
 //   moe_router_kernel   fp64 router logits (tree order) and sum |w x| per row
+//   moe_router_route_kernel  router and routing in one launch for up to 16
+//                       tokens (the last of a token's workgroups routes it)
 //   moe_route_kernel    per token: exact ranking (rows whose rounding
 //                       interval overlaps a top-(k+1) row are recomputed in
 //                       the reference's own order), softmax, top-k, weights;
@@ -35,21 +37,19 @@ namespace pyrite {
 
 constexpr int kMoeMaxE = 1024;  // experts supported by the route kernel
 constexpr int kMoeMaxK = 32;    // experts per token supported
+constexpr int kMoeFusedRouteBatch = 16;  // up to this batch, router and routing share one launch
 
 // ---------------------------------------------------------------- router
 
-// One wave per (expert row, token).  F32 routers (the Qwen3 case) read 4
-// weights per lane per load; other types decode element by element.
-__global__ __launch_bounds__(64) void moe_router_kernel(int type, const uint8_t* __restrict__ W,
-                                                        unsigned long long row_bytes, int E, int H, int bs, int bpb,
-                                                        const float* __restrict__ X, unsigned long long ldx,
-                                                        double* __restrict__ logits, double* __restrict__ mags) {
-    const int b = blockIdx.y;
-    const int e = blockIdx.x;
-    const int lane = threadIdx.x;
-    const uint8_t* rp = W + (unsigned long long)e * row_bytes;
-    const float* x = X + (unsigned long long)b * ldx;
-    double acc = 0.0, mag = 0.0;
+// Router logit of one (expert row, token) by one wave, fp64 products and tree
+// sums, with the sum of |products| for the rounding bound.  F32 routers (the
+// Qwen3 case) read 4 weights per lane per load; other types decode element by
+// element.  Every lane returns the totals.
+__device__ __forceinline__ void moe_router_row(int type, const uint8_t* __restrict__ rp, int H, int bs, int bpb,
+                                               const float* __restrict__ x, double& acc, double& mag) {
+    const int lane = threadIdx.x & 63;
+    acc = 0.0;
+    mag = 0.0;
     if (type == T_F32 && (H & 3) == 0 && ((reinterpret_cast<uintptr_t>(rp) | reinterpret_cast<uintptr_t>(x)) & 15) == 0) {
         const float4* w4 = reinterpret_cast<const float4*>(rp);
         const float4* x4 = reinterpret_cast<const float4*>(x);
@@ -71,7 +71,18 @@ __global__ __launch_bounds__(64) void moe_router_kernel(int type, const uint8_t*
         acc += __shfl_xor(acc, off, 64);
         mag += __shfl_xor(mag, off, 64);
     }
-    if (lane == 0) {
+}
+
+// One wave per (expert row, token).
+__global__ __launch_bounds__(64) void moe_router_kernel(int type, const uint8_t* __restrict__ W,
+                                                        unsigned long long row_bytes, int E, int H, int bs, int bpb,
+                                                        const float* __restrict__ X, unsigned long long ldx,
+                                                        double* __restrict__ logits, double* __restrict__ mags) {
+    const int b = blockIdx.y;
+    const int e = blockIdx.x;
+    double acc, mag;
+    moe_router_row(type, W + (unsigned long long)e * row_bytes, H, bs, bpb, X + (unsigned long long)b * ldx, acc, mag);
+    if (threadIdx.x == 0) {
         logits[(unsigned long long)b * E + e] = acc;
         mags[(unsigned long long)b * E + e] = mag;
     }
@@ -121,6 +132,7 @@ struct MoePlan {
     int* pair_tok;   // [max_pairs] token of each padded pair, -1 for padding
     int* pos;        // [batch * k] padded pair index of (token, slot)
     int* totals;     // [2]: padded pairs, chunks
+    int* chunk_e;    // [chunks] expert of each chunk; chunk c holds padded pairs [c * MB, (c + 1) * MB)
 };
 
 struct MoeRouteArgs {
@@ -148,8 +160,12 @@ __device__ __forceinline__ bool rank_before(double la, int a, double lb, int b) 
     return la > lb || (la == lb && a < b);
 }
 
-__global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
-    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// Routing of token t by a whole 256-thread workgroup: exact ranking, weights,
+// and (last token's workgroup) the plan.  CO: the logits were written by other
+// workgroups of the same launch and are read with device-coherent loads.
+template <bool CO>
+__device__ void moe_route_token(const MoeRouteArgs& a, const int t) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = a.E, k = a.k;
     __shared__ double s_l[kMoeMaxE];
     __shared__ double s_b[kMoeMaxE];
@@ -160,13 +176,19 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     __shared__ int s_poff[kMoeMaxE + 1];
     __shared__ int s_nmarked, s_last;
     const float* x = a.X + (unsigned long long)t * a.ldx;
+    __shared__ int s_rank[kMoeMaxE];
+    __shared__ double s_tl[kMoeMaxK + 1], s_tb[kMoeMaxK + 1];
+    __shared__ int s_slow;
+    __shared__ double s_total;
+    __shared__ double s_w[kMoeMaxK];
 
     // NaN logits rank last (as -inf), keeping the ranks a total order
     int nonfinite = 0;
     for (int e = tid; e < E; e += 256) {
-        const double l = a.logits[(unsigned long long)t * E + e];
+        const unsigned long long o = (unsigned long long)t * E + e;
+        const double l = CO ? ld_dev(a.logits + o) : a.logits[o];
         s_l[e] = isnan(l) ? -INFINITY : l;
-        s_b[e] = a.gamma * a.mags[(unsigned long long)t * E + e];
+        s_b[e] = a.gamma * (CO ? ld_dev(a.mags + o) : a.mags[o]);
         s_mark[e] = 0;
         nonfinite |= !isfinite(l) || !isfinite(s_b[e]);
     }
@@ -176,7 +198,6 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     // rank of every expert in (-logit, e) order (a total order: ranks are
     // unique); the first n land in s_top.  Up to 128 experts, two threads
     // count each expert's rank over half of the others each.
-    __shared__ int s_rank[kMoeMaxE];
     auto rank_top = [&](int n) {
         if (E <= 128) {  // block-uniform branch
             const int e = tid & 127, h = tid >> 7;
@@ -213,7 +234,6 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     {
         // the top rows' logits and bounds gathered next to their ids, so the
         // scan below reads them without a dependent lookup
-        __shared__ double s_tl[kMoeMaxK + 1], s_tb[kMoeMaxK + 1];
         if (tid < kk) {
             s_tl[tid] = s_l[s_top[tid]];
             s_tb[tid] = s_b[s_top[tid]];
@@ -261,23 +281,22 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     //    near the subnormal range), every row is recomputed exactly and the
     //    probabilities are formed as the reference forms them.  Non-finite
     //    logits keep the (-l, e) order, NaN last.
-    __shared__ int s_slow;
-    __shared__ double s_total;
-    if (tid == 0) {
-        int slow = 0;
-        if (!nonfinite) {
+    // one thread per pair (i, i + 1), i < k, i + 1 < kk
+    {
+        const int np = kk - 1 < k ? kk - 1 : k;
+        int bad = 0;
+        if (!nonfinite && tid < np) {
             const double l0 = s_l[s_top[0]], b0 = s_b[s_top[0]];
-            const int np = kk - 1 < k ? kk - 1 : k;  // pairs (i, i + 1), i < k, i + 1 < kk
-            for (int i = 0; i < np; ++i) {
-                const int ea = s_top[i], eb = s_top[i + 1];
-                const double la = s_l[ea], lb = s_l[eb], ba = s_b[ea], bb = s_b[eb];
-                if (ba == 0.0 && bb == 0.0 && la == lb) continue;  // equal exact logits: equal p, index order
+            const int ea = s_top[tid], eb = s_top[tid + 1];
+            const double la = s_l[ea], lb = s_l[eb], ba = s_b[ea], bb = s_b[eb];
+            if (!(ba == 0.0 && bb == 0.0 && la == lb)) {  // equal exact logits: equal p, index order
                 const double gap = (la - lb) - (ba + bb);
                 const double margin = 0x1p-48 * (1.0 + fabs(la - l0) + fabs(lb - l0) + b0 + ba + bb);
-                if (!(gap > margin) || lb - l0 < -700.0) slow = 1;
+                bad = !(gap > margin) || lb - l0 < -700.0;
             }
         }
-        s_slow = slow;
+        bad = __syncthreads_or(bad);
+        if (tid == 0) s_slow = bad;
     }
     __syncthreads();
     const bool slow = s_slow;
@@ -306,22 +325,22 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
         rank_top(k);  // by (-p, e) now
     }
 
-    // 4. the chosen probabilities: exact in the slow case; otherwise each
-    //    exp(l - peak) is the reference's formula and the total a tree sum
-    //    (which moves the weights by fp64 rounding only)
+    // 4. the chosen probabilities: exact in the slow case; otherwise the
+    //    device's exp (within an ulp of the host's) and a tree total, which
+    //    move the weights by fp64 rounding only
     const double peak = s_l[s_top[0]];
-    __shared__ double s_w[kMoeMaxK];
     if (!slow) {
         double tot = 0.0;
-        for (int e = tid; e < E; e += 256) tot += libm_exp(s_l[e] - peak);
+        for (int e = tid; e < E; e += 256) {
+            const double v = exp(s_l[e] - peak);
+            s_b[e] = v;  // the bounds are no longer needed
+            tot += v;
+        }
         for (int off = 32; off > 0; off >>= 1) tot += __shfl_xor(tot, off, 64);
         if (lane == 0) s_red[wave] = tot;
         __syncthreads();
         const double total = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-        if (tid < k) {
-            const int e = s_top[tid];
-            s_w[tid] = total <= 0.0 ? 1.0 / (double)E : libm_exp(s_l[e] - peak) / total;
-        }
+        if (tid < k) s_w[tid] = total <= 0.0 ? 1.0 / (double)E : s_b[s_top[tid]] / total;
     } else if (tid < k) {
         s_w[tid] = s_l[s_top[tid]];
     }
@@ -374,6 +393,7 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
             for (int j = 0; j < k; ++j) below += s_top[j] < s_top[tid];
             p.pair_tok[below] = 0;
             p.pos[tid] = below;
+            p.chunk_e[below] = s_top[tid];
         }
         if (tid == 0) {
             p.totals[0] = k;
@@ -446,7 +466,12 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
             p.totals[1] = tc;
         }
         __syncthreads();
-        for (int e = tid; e < E; e += 256) s_cnt[e] = s_poff[e];  // fill cursors
+        // padded pair offsets are multiples of MB, so expert e owns chunks
+        // [poff[e] / MB, poff[e + 1] / MB)
+        for (int e = tid; e < E; e += 256) {
+            s_cnt[e] = s_poff[e];  // fill cursors
+            for (int c = s_poff[e] / a.MB; c < s_poff[e + 1] / a.MB; ++c) p.chunk_e[c] = e;
+        }
         __syncthreads();
     }
     for (int q = tid; q < npairs; q += 256) {
@@ -458,6 +483,34 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) {
     for (int e = tid; e < E; e += 256)
         for (int q = s_cnt[e]; q < s_poff[e + 1]; ++q) p.pair_tok[q] = -1;
     if (tid == 0) st_dev(a.arrive, 0u);
+}
+
+__global__ __launch_bounds__(256) void moe_route_kernel(const MoeRouteArgs a) { moe_route_token<false>(a, blockIdx.x); }
+
+// Router and routing in one launch (small batches): workgroup (x, t) computes
+// the logits of experts 4x .. 4x + 3 (one per wave) for token t; the last of
+// token t's workgroups to arrive routes the token.  tok_arrive[t] is zero
+// before the launch and is left at zero.
+__global__ __launch_bounds__(256) void moe_router_route_kernel(const MoeRouteArgs a, unsigned* tok_arrive) {
+    const int t = blockIdx.y, wave = threadIdx.x >> 6;
+    const int e = blockIdx.x * 4 + wave;
+    if (e < a.E) {  // wave-uniform
+        double acc, mag;
+        moe_router_row(a.type, a.W + (unsigned long long)e * a.row_bytes, a.H, a.bs, a.bpb,
+                       a.X + (unsigned long long)t * a.ldx, acc, mag);
+        if ((threadIdx.x & 63) == 0) {
+            st_dev(const_cast<double*>(a.logits) + (unsigned long long)t * a.E + e, acc);
+            st_dev(const_cast<double*>(a.mags) + (unsigned long long)t * a.E + e, mag);
+        }
+    }
+    drain_dev();  // this workgroup's logits have completed before its arrival
+    __syncthreads();
+    __shared__ int s_go;
+    if (threadIdx.x == 0) s_go = arrive_dev(tok_arrive + t) == gridDim.x - 1;
+    __syncthreads();
+    if (!s_go) return;
+    if (threadIdx.x == 0) st_dev(tok_arrive + t, 0u);
+    moe_route_token<true>(a, t);
 }
 
 // ---------------------------------------------------------------- gather, swiglu, combine
@@ -490,12 +543,20 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     const int t = blockIdx.y;
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= H) return;
+    // every slot's weight, position and value are requested before the sum
+    // (independent loads in flight together), then summed in slot order
+    double w[kMoeMaxK];
+    float y[kMoeMaxK];
+#pragma unroll
+    for (int s = 0; s < kMoeMaxK; ++s)
+        if (s < k) {
+            w[s] = wts[(unsigned long long)t * k + s];
+            y[s] = YD[(unsigned long long)pos[(unsigned long long)t * k + s] * H + i];
+        }
     double acc = 0.0;
-    for (int s = 0; s < k; ++s) {
-        const double w = wts[(unsigned long long)t * k + s];
-        if (w == 0.0) continue;
-        acc += w * (double)YD[(unsigned long long)pos[(unsigned long long)t * k + s] * H + i];
-    }
+#pragma unroll
+    for (int s = 0; s < kMoeMaxK; ++s)
+        if (s < k && w[s] != 0.0) acc += w[s] * (double)y[s];
     out[(unsigned long long)t * ldo + i] = (float)acc;
 }
 
@@ -515,8 +576,7 @@ struct MoeMvArgs {
     MoeMat m[2];
     int nm;
     int tile;                   // rows per item
-    const int* coff;            // [E + 1] chunk offsets
-    const int* poff;            // [E + 1] padded pair offsets
+    const int* chunk_e;         // [chunks] expert of each chunk (its pairs start at chunk * MB)
     const int* totals;          // [1]: chunks
     int E;
     const int* pair_tok;        // XGather: token of each padded pair
@@ -543,13 +603,8 @@ __global__ __launch_bounds__(kMvThreads) void moe_mv_kernel(const MoeMvArgs a) {
         const MoeMat& m = a.m[j];
         const int chunk = (int)(r / tiles[j]);
         const int tile = (int)(r - (long long)chunk * tiles[j]);
-        int lo = 0, hi = a.E;  // expert e with coff[e] <= chunk < coff[e + 1]
-        while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (a.coff[mid] <= chunk) lo = mid; else hi = mid;
-        }
-        const int e = lo;
-        const int pair0 = a.poff[e] + (chunk - a.coff[e]) * MB;
+        const int e = a.chunk_e[chunk];
+        const int pair0 = chunk * MB;
         const int row0 = tile * a.tile;
         MvDesc d;
         d.W = m.W + (unsigned long long)e * m.slice + (unsigned long long)row0 * m.row_bytes;
@@ -732,8 +787,7 @@ struct MoeMxArgs {
     const float* act;           // [pairs][cols] silu(gate) * up (moe_dn_kernel)
     unsigned* amax;             // [pairs] largest finite |act| (ordered uint bits)
     float* Y;                   // moe_gu_kernel: act [pairs][rows]; moe_dn_kernel: [pairs][rows]
-    const int* coff;
-    const int* poff;
+    const int* chunk_e;         // expert of each chunk (its pairs start at chunk * kMoeMxTok)
     const int* totals;
     int E;
 };
@@ -743,26 +797,16 @@ __device__ __forceinline__ float moe_act(float g, float u) {
     return g > -60.f ? g / (1.f + expf(-g)) * u : 0.f;
 }
 
-__device__ __forceinline__ int moe_expert_of(const int* coff, int E, int chunk) {
-    int lo = 0, hi = E;  // expert e with coff[e] <= chunk < coff[e + 1]
-    while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (coff[mid] <= chunk) lo = mid; else hi = mid;
-    }
-    return lo;
-}
-
 // One workgroup per chunk: the gathered tokens' fragments, exponents, and the
 // chunk's act maxima cleared for moe_gu_kernel.
 __global__ __launch_bounds__(256) void moe_xfrag_kernel(const float* X, unsigned long long ldx, int cols,
-                                                        const int* pair_tok, const int* coff, const int* poff,
-                                                        const int* totals, int E, int kmode, uint4* xf, int* xe,
+                                                        const int* pair_tok, const int* totals, int kmode,
+                                                        uint4* xf, int* xe,
                                                         unsigned* amax) {
     __shared__ unsigned tok_max[kMoeMxTok];
     const int chunk = blockIdx.x;
     if (chunk >= totals[1]) return;
-    const int e = moe_expert_of(coff, E, chunk);
-    const int pair0 = poff[e] + (chunk - coff[e]) * kMoeMxTok;
+    const int pair0 = chunk * kMoeMxTok;
     const int tid = threadIdx.x;
     if (tid < kMoeMxTok) {
         tok_max[tid] = 0u;
@@ -905,8 +949,8 @@ __global__ __launch_bounds__(256, 2) void moe_gu_kernel(const MoeMxArgs a) {
     int staged = -1;
     for (long long it = it0; it < it1; ++it) {
         const int chunk = (int)(it / a.parts), part = (int)(it - (long long)chunk * a.parts);
-        const int e = moe_expert_of(a.coff, a.E, chunk);
-        const int pair0 = a.poff[e] + (chunk - a.coff[e]) * kMoeMxTok;
+        const int e = a.chunk_e[chunk];
+        const int pair0 = chunk * kMoeMxTok;
         __syncthreads();  // the previous item's waves are done with the fragments and results
         if (chunk != staged) {
             const uint4* src = a.xf + (size_t)chunk * steps * 64;
@@ -964,8 +1008,8 @@ __global__ __launch_bounds__(256, 2) void moe_dn_kernel(const MoeMxArgs a) {
     int staged = -1;
     for (long long it = it0; it < it1; ++it) {
         const int chunk = (int)(it / a.parts), part = (int)(it - (long long)chunk * a.parts);
-        const int e = moe_expert_of(a.coff, a.E, chunk);
-        const int pair0 = a.poff[e] + (chunk - a.coff[e]) * kMoeMxTok;
+        const int e = a.chunk_e[chunk];
+        const int pair0 = chunk * kMoeMxTok;
         __syncthreads();  // the previous item's waves are done with the fragments and results
         if (chunk != staged) {
             const int count = steps * 4 * kMoeMxTok;
@@ -1102,6 +1146,7 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
         p->pair_tok = cv.take<int>(max_pairs);
         p->pos = cv.take<int>(batch * K);
         p->totals = cv.take<int>(2);
+        p->chunk_e = cv.take<int>(max_pairs);
         *xg = cv.take<float>(max_pairs * H);
         *g = cv.take<float>(max_pairs * I);
         *u = cv.take<float>(max_pairs * I);
@@ -1118,12 +1163,7 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     Carver cw{static_cast<char*>(ws->base)};
     layout(cw, &logits, &mags, &ids, &wts, &plan, &xg, &g, &u, &act, &yd);
 
-    // 1. router
-    hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)E, (unsigned)batch), dim3(64), 0, stream,
-                       L.router_type, static_cast<const uint8_t*>(L.router), (unsigned long long)rr, (int)E, (int)H,
-                       gr.bs, gr.bpb, X, (unsigned long long)ldx, logits, mags);
-    if (hipGetLastError() != hipSuccess) return -4;
-    // 2. route + plan
+    // 1. router logits, 2. route + plan (one launch for small batches)
     MoeRouteArgs ra;
     ra.type = L.router_type;
     ra.W = static_cast<const uint8_t*>(L.router);
@@ -1153,7 +1193,17 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     ra.batch = (int)batch;
     ra.arrive = static_cast<unsigned int*>(ws->arrive);
     ra.plan = plan;
-    hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)batch), dim3(256), 0, stream, ra);
+    if (batch <= kMoeFusedRouteBatch) {
+        // counters 1 .. batch of the zeroed arrival block (0 is the token counter)
+        hipLaunchKernelGGL(moe_router_route_kernel, dim3((unsigned)((E + 3) / 4), (unsigned)batch), dim3(256), 0,
+                           stream, ra, static_cast<unsigned int*>(ws->arrive) + 1);
+    } else {
+        hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)E, (unsigned)batch), dim3(64), 0, stream,
+                           L.router_type, static_cast<const uint8_t*>(L.router), (unsigned long long)rr, (int)E,
+                           (int)H, gr.bs, gr.bpb, X, (unsigned long long)ldx, logits, mags);
+        if (hipGetLastError() != hipSuccess) return -4;
+        hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)batch), dim3(256), 0, stream, ra);
+    }
     if (hipGetLastError() != hipSuccess) return -4;
     if (mfma) {
         // 3. fragments of each chunk's tokens; 4. gate and up with silu(gate) * up;
@@ -1164,12 +1214,11 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
         const int grid = 2 * dev_info().cus;
         const size_t est_chunks = E < batch * K ? E : batch * K;
         hipLaunchKernelGGL(moe_xfrag_kernel, dim3((unsigned)max_chunks), dim3(256), 0, stream, X,
-                           (unsigned long long)ldx, (int)H, plan.pair_tok, plan.coff, plan.poff, plan.totals, (int)E,
+                           (unsigned long long)ldx, (int)H, plan.pair_tok, plan.totals,
                            moe_kmode(L.gate_type), xf, xe, amax);
         if (hipGetLastError() != hipSuccess) return -4;
         MoeMxArgs xa;
-        xa.coff = plan.coff;
-        xa.poff = plan.poff;
+        xa.chunk_e = plan.chunk_e;
         xa.totals = plan.totals;
         xa.E = (int)E;
         xa.xf = xf;
@@ -1232,8 +1281,7 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     };
     const bool al_gu = ((reinterpret_cast<uintptr_t>(L.gate) | reinterpret_cast<uintptr_t>(L.up)) & 3u) == 0;
     MoeMvArgs ma;
-    ma.coff = plan.coff;
-    ma.poff = plan.poff;
+    ma.chunk_e = plan.chunk_e;
     ma.totals = plan.totals;
     ma.E = (int)E;
     ma.pair_tok = plan.pair_tok;
