@@ -539,13 +539,22 @@ def run_llama_step(lib, sptr, arrs, batch, c):
             raise RuntimeError(f"{key} launch failed: {rc} {lib.pyrite_hip_last_error()}")
 
 
+LLAMA_WORKLOAD = ("Llama-3-8B layer, Q4_K_M mix: q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096 Q4_K, "
+                  "down 4096x14336 Q6_K")
+
+
 def bench_llama(torch, np, quantize, stream, device, lib, sptr, mats):
     """Llama-3-8B layer in Q4_K_M mix: its q, gate and down matrices alone at batch 1,
     and the 512-token prefill (four launches, MFMA dequant-GEMM)."""
-    layer_bytes = sum(p.nbytes for _, _, _, p in mats.values())
-    res = {"workload": "Llama-3-8B layer, Q4_K_M mix: q/o 4096x4096, k/v 1024x4096, gate/up 14336x4096 Q4_K, "
-                       "down 4096x14336 Q6_K", "bytes_per_layer": layer_bytes}
-    # prefill: 2 weight copies, 2 steps per graph
+    res = {"workload": LLAMA_WORKLOAD, "bytes_per_layer": sum(p.nbytes for _, _, _, p in mats.values())}
+    res["prefill_512"] = bench_llama_prefill(torch, np, stream, lib, sptr, mats)
+    res["decode_b1_matrices"] = bench_llama_singles(torch, np, stream, device, lib, sptr, mats)
+    return res
+
+
+def bench_llama_prefill(torch, np, stream, lib, sptr, mats):
+    """The layer's 512-token prefill: four grouped launches (MFMA dequant-GEMM)."""
+    # 2 weight copies, 2 steps per graph
     copies = [{n: torch.from_numpy(m[3]).cuda() for n, m in mats.items()} for _ in range(2)]
     batch = 512
     arrs, xs, ys = llama_step_descs(np, torch, mats, batch, copies)
@@ -560,7 +569,7 @@ def bench_llama(torch, np, quantize, stream, device, lib, sptr, mats):
                     "frac_of_mfma_peak": round(f / avg[key] / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)}
     dom = max(per, key=lambda k: avg[k])
     fd = 2.0 * batch * sum(mats[n][1] * mats[n][2] for n in dict((k, nm) for k, _, nm, _ in DECODE_LAUNCHES)[dom])
-    res["prefill_512"] = {"us": round(dt * 1e6, 2), "tflops": round(flops / dt / 1e12, 2),
+    res = {"us": round(dt * 1e6, 2), "tflops": round(flops / dt / 1e12, 2),
                           "per_launch": per,
                           "roofline": {"bound": "mfma", "achieved": round(fd / avg[dom] / 1e12, 1),
                                        "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
@@ -570,8 +579,12 @@ def bench_llama(torch, np, quantize, stream, device, lib, sptr, mats):
                                        "timing": TIMING}}
     del copies, arrs, xs, ys
     torch.cuda.empty_cache()
-    # The layer's distinct matrix shapes alone at batch 1, each over rotated
-    # copies of more than 600 MB (beyond the 256 MB Infinity Cache).
+    return res
+
+
+def bench_llama_singles(torch, np, stream, device, lib, sptr, mats):
+    """The layer's distinct matrix shapes alone at batch 1, each over rotated
+    copies of more than 600 MB (beyond the 256 MB Infinity Cache)."""
     singles = {}
     for name in ("q", "gate", "down"):
         t, rows, cols, p = mats[name]
@@ -590,8 +603,7 @@ def bench_llama(torch, np, quantize, stream, device, lib, sptr, mats):
             "roofline": roofline_hbm(p.nbytes, avg1, load_traffic("traffic_llama_decode", name),
                                      kernel=f"mv_kernel (VALU) {label} batch 1", timing=TIMING)}
         del ws1, first
-    res["decode_b1_matrices"] = singles
-    return res
+    return singles
 
 
 def main() -> int:
@@ -605,7 +617,7 @@ def main() -> int:
     ap.add_argument("--only", default=None,
                     help="run only one workload and print its JSON, for profiling: llama_decode (the headline "
                          "launches, eagerly), q4k_3072x1024, sweep, lm_head_q6k_151936x1024, moe_qwen3_30b_a3b, "
-                         "llama3_8b_layer, gguf_upload, copy_calibration")
+                         "llama3_8b_layer, llama3_8b_prefill, gguf_upload, copy_calibration")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures the dequant-matvec path on one GPU; runs on more than one GPU "
@@ -634,6 +646,7 @@ def main() -> int:
         "moe_qwen3_30b_a3b": lambda: bench_moe(torch, np, quantize, stream, device),
         "llama3_8b_layer": lambda: bench_llama(torch, np, quantize, stream, device, lib, sptr,
                                                llama_weights(np, quantize)),
+        "llama3_8b_prefill": lambda: bench_llama_prefill(torch, np, stream, lib, sptr, llama_weights(np, quantize)),
         "gguf_upload": lambda: bench_gguf_upload(torch, np),
         "copy_calibration": lambda: copy_calibration(torch, stream),
     }

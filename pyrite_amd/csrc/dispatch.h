@@ -71,9 +71,10 @@ bool mx_type_supported(int type);
 int mx_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, size_t done, bool al,
                     hipStream_t stream, hipEvent_t start, hipEvent_t stop);
 
-// mg.hip: MFMA dequant-GEMM for large batches (arguments already validated).
-int mg_launch(int type, const MatvecArgs& m, size_t batch, bool al, hipStream_t stream, hipEvent_t start,
-              hipEvent_t stop);
+// mg.hip: MFMA dequant-GEMM for large batches (arguments already validated);
+// consecutive matrices with the same activations share a launch.
+int mg_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, bool al, hipStream_t stream,
+                    hipEvent_t start, hipEvent_t stop);
 
 // matvec.hip: Y[b][r] = sum_c W[r][c] X[b][c] in fp32, any batch (chunked by 8).
 // Returns 0, -1 (type), -2 (geometry), -3 (pointer/length/alignment), -4 (launch).

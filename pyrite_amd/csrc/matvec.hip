@@ -18,15 +18,8 @@ int matvec_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch
     // the MFMA kernels address a 32-row tile's weights with 32-bit offsets
     const bool mfma = g.bs > 1 && !forced && mx_type_supported(type) &&
                       32ull * (max_cols / g.bs * g.bpb) + 16 < 0x7FFFFFFFull;
-    // prefill-sized batches: the MFMA dequant-GEMM, one launch per matrix
-    if (mfma && batch >= kGemmMinBatch) {
-        for (size_t i = 0; i < n; ++i) {
-            const int rc = mg_launch(type, mats[i], batch, al, stream, i == 0 ? start : nullptr,
-                                     i + 1 == n ? stop : nullptr);
-            if (rc != 0) return rc;
-        }
-        return 0;
-    }
+    // prefill-sized batches: the MFMA dequant-GEMM (matrices sharing activations share a launch)
+    if (mfma && batch >= kGemmMinBatch) return mg_group_launch(type, mats, n, batch, al, stream, start, stop);
     if (mfma && batch >= 3) {
         for (size_t done = 0; done < batch; done += 8) {
             const size_t c = batch - done < 8 ? batch - done : 8;

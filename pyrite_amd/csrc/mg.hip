@@ -5,234 +5,433 @@
 // Operands and exact fp16 fragments are those of mx_traits.h: A = activations
 // (MFMA row m = 2t + p, fp16 hi (p = 0) and lo (p = 1) parts of x[t]), B =
 // weights built exactly from the block codes, D = per lane row r0 + n of W and
-// token-parts 4g..4g+3.  The block scales are applied once per block (epi).
+// token-parts 4g..4g+3.  The block scales are applied once per block.
 //
-// Schedule: a workgroup owns 128 rows of W (each of its 4 waves 32 rows = two
-// 16-row MFMA tiles) and 32 tokens (four 8-token A sub-tiles).  It walks K in
-// chunks of 8 steps (256 columns): the chunk's activations are converted to
-// fp16 hi/lo fragments in LDS once for the workgroup, and each wave decodes
-// each weight block once into B fragments and multiplies them against all
-// four token sub-tiles.  A wave loads its next block while it computes the
-// current one.  Workgroups with the same rows and consecutive token tiles are
-// adjacent in the grid, so the weights they share are read from HBM once.
-// Each token's activations are staged scaled by a per-(token, chunk) power of
-// two that brings their largest finite |x| into [2^14, 2^15) (no fp16
-// overflow, full hi/lo precision at any scale); the block epilogue multiplies
-// it back (exact).
+// Three launches:
+//   mg_exp_kernel   one wave per token: the power of two e_t that brings the
+//                   token's largest finite |x| into [2^14, 2^15);
+//   mg_frag_kernel  x[t] * 2^-e_t as fp16 hi/lo A fragments, written in the
+//                   order the GEMM reads them: XF[(xs * Fp + f) * 64 + lane]
+//                   is lane `lane`'s 16 bytes of fragment step xs for tokens
+//                   8f..8f+7 (1 KiB per fragment).  Fragment steps are the
+//                   32-column steps, and for formats with per-sub-block mins
+//                   (MINSUM) one more per block: the tokens' sums over each
+//                   32-column sub-block, times 2^-e_t-5, in K-slots 0..7;
+//   mg_kernel       the GEMM.  A workgroup of 8 waves owns 256 rows of one
+//                   matrix (32 per wave = two 16-row MFMA tiles) and 8 * TF
+//                   tokens.  K is walked in chunks of 8 steps: the chunk's
+//                   fragments go from XF into LDS by direct global -> LDS
+//                   loads (no registers), one chunk ahead, and each wave
+//                   builds each weight block's B fragments once (codes loaded
+//                   one block ahead into registers) and multiplies them
+//                   against all TF token fragments.  MINSUM formats take
+//                   their min term as one MFMA per block against the staged
+//                   sums.  The result is scaled by 2^e_t once, at the end.
+// Two waves per SIMD (at most 256 registers each) let one wave's fragment
+// building run under the other's MFMAs.  Workgroups are mapped so that all
+// token tiles of one row tile run on one XCD, next to each other: their
+// shared weights are read into that XCD's L2 once.  Up to four matrices with
+// the same activations and columns share a launch (row tiles concatenated).
 #include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "dispatch.h"
 #include "mx_traits.h"
 
 namespace pyrite {
 
-constexpr int kMgRows = 128;      // rows per workgroup
-constexpr int kMgTok = 32;        // tokens per workgroup
-constexpr int kMgSub = kMgTok / 8;
-constexpr int kMgChunkSteps = 8;  // 32-column steps per staged chunk
+constexpr int kMgWaves = 8;
+constexpr int kMgWaveTiles = 2;                         // 16-row tiles per wave
+constexpr int kMgRows = 16 * kMgWaveTiles * kMgWaves;   // rows per workgroup
+constexpr int kMgChunk = 8;                             // 32-column steps staged per chunk
+constexpr int kMgMaxMats = 4;
 
-struct MgArgs {
+template <class F, class = void> struct MgMinSum : std::false_type {};
+template <class F> struct MgMinSum<F, std::void_t<decltype(F::MINSUM)>> : std::bool_constant<F::MINSUM> {};
+
+// fragment steps per block: the 32-column steps, plus the sums step (MINSUM)
+template <class F>
+constexpr int mg_xs_per_block() { return F::STEPS + (MgMinSum<F>::value ? 1 : 0); }
+
+// 8-token fragments per workgroup: 8 for MINSUM formats (one accumulator per
+// block), 4 for the others (two), so that a wave fits in 256 registers
+template <class F>
+constexpr int mg_tf() { return MgMinSum<F>::value ? 8 : 4; }
+
+struct MgMat {
     const uint8_t* W;
     unsigned long long row_bytes;
-    const float* X;
-    unsigned long long ldx;
     float* Y;
     unsigned long long ldy;
-    int rows, cols, batch;
+    int rows;
+    int tile0;  // first row tile of this matrix in the launch
+};
+
+struct MgArgs {
+    MgMat m[kMgMaxMats];
+    int nmat;
+    const uint4* XF;
+    const int* texp;
+    int Fp;  // fragments per fragment step in XF (token tiles * TF)
+    int cols, batch;
     int row_tiles, tok_tiles;
 };
 
-__device__ __forceinline__ void mg_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+// ---------------------------------------------------------------- activations
+// One workgroup per token: its largest finite |x|, every load issued before
+// the reduction.
+__global__ __launch_bounds__(256) void mg_exp_kernel(const float* __restrict__ X, unsigned long long ldx, int cols,
+                                                     int* __restrict__ texp) {
+    __shared__ float red[4];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float* row = X + (unsigned long long)t * ldx;
+    float m = 0.f;
+    for (int c0 = 4 * tid; c0 < cols; c0 += 1024 * 8) {
+        float4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int c = c0 + 1024 * k;
+            v[k] = c < cols ? ld_x4(row + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float a[4] = {fabsf(v[k].x), fabsf(v[k].y), fabsf(v[k].z), fabsf(v[k].w)};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) m = fmaxf(m, a[i] <= 3.402823466e38f ? a[i] : 0.f);
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) texp[t] = norm_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
+}
+
+// Workgroup (token fragment f, 256-column window sb): the 8 tokens' window
+// is read row by row into LDS, then thread (step s, K-slot group g, token
+// 8f + tp) writes the hi and lo 16 bytes of its 8 columns.  MINSUM formats
+// (256-column blocks, K-slot map 1) also write the block's sums step: lane
+// group 0, rows 2 tp + p hold the hi / lo parts of the token's eight
+// sub-block sums (times 2^-e_t-5), the other lanes zeros.
+template <int T>
+__global__ __launch_bounds__(256) void mg_frag_kernel(const float* __restrict__ X, unsigned long long ldx, int cols,
+                                                      int batch, const int* __restrict__ texp, uint4* __restrict__ XF,
+                                                      int Fp) {
+    using F = Mx<T>;
+    constexpr bool MS = MgMinSum<F>::value;
+    constexpr int KM = MxKMode<F>::value;
+    constexpr int XPB = mg_xs_per_block<F>();
+    constexpr int LD = 256 + 4;  // LDS row pitch (floats)
+    static_assert(!MS || (F::STEPS == 8 && KM == 1), "sums step: 256-column blocks, K-slot map 1");
+    __shared__ float xs[8 * LD];
+    __shared__ float sums[MS ? 64 : 1];
+    const int tid = threadIdx.x, nsteps = cols / 32, sg = (nsteps + 7) / 8;
+    const int f = blockIdx.x / sg, sb = blockIdx.x - f * sg;
+    {
+        const int tr = tid >> 5, c = 256 * sb + 8 * (tid & 31);
+        float4 u = make_float4(0.f, 0.f, 0.f, 0.f), w = u;
+        if (8 * f + tr < batch && c < cols) {
+            const float* q = X + (unsigned long long)(8 * f + tr) * ldx + c;
+            u = ld_x4(q);
+            w = ld_x4(q + 4);
+        }
+        float* d = xs + tr * LD + 8 * (tid & 31);
+        *reinterpret_cast<float4*>(d) = u;
+        *reinterpret_cast<float4*>(d + 4) = w;
+    }
+    __syncthreads();
+    const int sl = tid >> 5, tp = tid & 7, g = (tid >> 3) & 3;
+    const int t = 8 * f + tp;
+    const int e = t < batch ? texp[t] : 0;
+    if (8 * sb + sl < nsteps) {
+        const int off = KM == 1 ? 64 * g + 8 * sl : 32 * sl + 8 * g;
+        const float4 u = *reinterpret_cast<const float4*>(xs + tp * LD + off);
+        const float4 w = *reinterpret_cast<const float4*>(xs + tp * LD + off + 4);
+        const float v[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+        uint4 hi, lo;
+        split8(v, e, hi, lo);
+        const int xstep = MS ? sb * XPB + sl : 8 * sb + sl;
+        uint4* o = XF + ((size_t)xstep * Fp + f) * 64 + g * 16 + 2 * tp;
+        o[0] = hi;
+        o[1] = lo;
+    }
+    if constexpr (MS) {
+        if (tid < 64) {
+            // sub-block j = tid & 7 of token tid >> 3: columns 32 j .. 32 j + 31
+            const float* q = xs + (tid >> 3) * LD + 32 * (tid & 7);
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < 32; k += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(q + k);
+                acc += (v.x + v.y) + (v.z + v.w);
+            }
+            sums[tid] = acc;
+        }
+        __syncthreads();
+        if (tid < 64) {
+            uint4 r = make_uint4(0u, 0u, 0u, 0u);
+            if (tid < 16) {
+                const int tq = tid >> 1, tk = 8 * f + tq;
+                float sv[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) sv[j] = sums[tq * 8 + j];
+                uint4 hi, lo;
+                split8(sv, (tk < batch ? texp[tk] : 0) + 5, hi, lo);
+                r = (tid & 1) ? lo : hi;
+            }
+            XF[((size_t)(sb * XPB + 8) * Fp + f) * 64 + tid] = r;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- GEMM
+typedef __attribute__((address_space(3))) void lds_void;
+
+// 64 lanes x 16 bytes from src (per lane) to dst .. dst + 1 KiB (wave-uniform)
+__device__ __forceinline__ void lds_load_1k(const uint4* src, uint4* dst) {
+    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (lds_void*)(dst), 16, 0, 0);
+}
+
+__device__ __forceinline__ h8v as_h8(const uint4 v) {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    return __builtin_bit_cast(h8v, w);
 }
 
 template <int T, bool AL>
-__global__ __launch_bounds__(256) void mg_kernel(const MgArgs a) {
+__global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
     using F = Mx<T>;
-    constexpr int BPC = kMgChunkSteps / F::STEPS > 0 ? kMgChunkSteps / F::STEPS : 1;  // blocks per chunk
-    constexpr int CS = BPC * F::STEPS;                                               // steps per chunk
-    constexpr int XI = CS * 4 * kMgTok / 256;  // staged items (8 values of one token) per thread
-    __shared__ uint4 frag[CS * 4 * 64];
-    __shared__ unsigned tok_max[2][kMgTok];  // per chunk parity: largest finite |x| per token
+    constexpr bool MS = MgMinSum<F>::value;
+    constexpr int NT = kMgWaveTiles, TF = mg_tf<F>();
+    constexpr int NA = MS ? 1 : F::NACC;                                 // accumulators per block
+    constexpr int BPC = F::STEPS >= kMgChunk ? 1 : kMgChunk / F::STEPS;  // blocks per chunk
+    constexpr int XPB = mg_xs_per_block<F>();
+    constexpr int CX = BPC * XPB;  // fragment steps per chunk
+    constexpr int CF = CX * TF;    // fragments per chunk
+    // unaligned super-blocks: loads at the spans' own byte addresses
+    constexpr bool UA = !AL && F::BS == 256;
+    __shared__ uint4 abuf[2][CF * 64];
+
+    // XCD-aware order: workgroup b runs on XCD b % 8; logical tile L counts
+    // each XCD's workgroups contiguously, so the token tiles of a row tile
+    // share an XCD and run next to each other.
+    const int N = a.row_tiles * a.tok_tiles;
+    const int bx = blockIdx.x, xcd = bx & 7, per = N >> 3, rem = N & 7;
+    const int L = xcd * per + (xcd < rem ? xcd : rem) + (bx >> 3);
+    const int rt = L / a.tok_tiles, tt = L - rt * a.tok_tiles;
+
+    // matrix of this row tile (workgroup-uniform)
+    const uint8_t* W = a.m[0].W;
+    unsigned long long row_bytes = a.m[0].row_bytes, ldy = a.m[0].ldy;
+    float* Y = a.m[0].Y;
+    int rows = a.m[0].rows, tile0 = 0;
+#pragma unroll
+    for (int k = 1; k < kMgMaxMats; ++k) {
+        if (k < a.nmat && rt >= a.m[k].tile0) {
+            W = a.m[k].W;
+            row_bytes = a.m[k].row_bytes;
+            ldy = a.m[k].ldy;
+            Y = a.m[k].Y;
+            rows = a.m[k].rows;
+            tile0 = a.m[k].tile0;
+        }
+    }
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
-    const int rt = blockIdx.x / a.tok_tiles, tt = blockIdx.x - rt * a.tok_tiles;
-    const int tok0 = tt * kMgTok;
-    const long long r0 = (long long)rt * kMgRows + 32 * w + n, r1 = r0 + 16;
-    const uint8_t* rp0 = a.W + (r0 < a.rows ? r0 : a.rows - 1) * a.row_bytes;
-    const uint8_t* rp1 = a.W + (r1 < a.rows ? r1 : a.rows - 1) * a.row_bytes;
+    const long long rbase = (long long)(rt - tile0) * kMgRows + 16 * NT * w + n;
+    const uint8_t* rp[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+        const long long r = rbase + 16 * i;
+        rp[i] = W + (r < rows ? r : rows - 1) * row_bytes;
+    }
     const int nblk = a.cols / F::BS;
     const int nchunk = (nblk + BPC - 1) / BPC;
-    // staging role: token tl, column group xg (8 columns) of steps xs0 + 2k
-    const int tl = tid & 31, xg = (tid >> 5) & 3, xs0 = tid >> 7;
-    const bool tok_ok = tok0 + tl < a.batch;
-    const float* xrow = a.X + (unsigned long long)(tok_ok ? tok0 + tl : 0) * a.ldx;
+    const int nxs = nblk * XPB;
+    const uint4* xsrc = a.XF + (size_t)tt * TF * 64 + lane;
 
-    f4v acc[kMgSub][2];
+    // the chunk's fragments: fragment j = (fragment step j / TF, token fragment j % TF)
+    auto stage = [&](int ch, int buf) {
+        const int x0 = ch * CX;
+        const int nx = nxs - x0 < CX ? nxs - x0 : CX;
 #pragma unroll
-    for (int s = 0; s < kMgSub; ++s) acc[s][0] = acc[s][1] = f4v{0.f, 0.f, 0.f, 0.f};
-    if (tid < kMgTok) tok_max[0][tid] = 0u;
+        for (int k = 0; k < (CF + kMgWaves - 1) / kMgWaves; ++k) {
+            const int j = w + kMgWaves * k;
+            const int xl = j / TF, fl = j - xl * TF;
+            if (j < CF && xl < nx) lds_load_1k(xsrc + ((size_t)(x0 + xl) * a.Fp + fl) * 64, &abuf[buf][j * 64]);
+        }
+    };
 
-    typename F::Raw ca, cb, na, nb;
-    F::template load<AL>(rp0, g, ca);
-    F::template load<AL>(rp1, g, cb);
+    typename F::Raw ca[NT], na[NT];
+#pragma unroll
+    for (int i = 0; i < NT; ++i) F::template load<AL, false, UA>(rp[i], g, ca[i]);
+    stage(0, 0);
+
+    f4v acc[TF][NT];
+#pragma unroll
+    for (int f = 0; f < TF; ++f)
+#pragma unroll
+        for (int i = 0; i < NT; ++i) acc[f][i] = f4v{0.f, 0.f, 0.f, 0.f};
 
     for (int ch = 0; ch < nchunk; ++ch) {
+        // this chunk's fragments have landed (all waves), and every wave is
+        // done with the buffer the next chunk goes into
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (ch + 1 < nchunk) stage(ch + 1, (ch + 1) & 1);
+        const uint4* ab = abuf[ch & 1] + lane;
         const int b0 = ch * BPC;
         const int b1 = b0 + BPC < nblk ? b0 + BPC : nblk;
-        const int s0 = b0 * F::STEPS, ns = (b1 - b0) * F::STEPS;
-        unsigned* tmax = tok_max[ch & 1];
-        // Stage the chunk: activations into registers, each token's largest
-        // finite |x| into LDS, then fp16 hi/lo fragments of x * 2^-e with the
-        // token's normalising exponent e (the epilogue multiplies by 2^e).
-        float xv[XI][8];
-        float mx = 0.f;
-#pragma unroll
-        for (int k = 0; k < XI; ++k) {
-            const int st = xs0 + 2 * k;
-            if (tok_ok && st < ns) {
-                const float* q = xrow + mx_col<F>(s0 + st, xg);
-                const float4 u = ld_x4(q), v = ld_x4(q + 4);
-                xv[k][0] = u.x; xv[k][1] = u.y; xv[k][2] = u.z; xv[k][3] = u.w;
-                xv[k][4] = v.x; xv[k][5] = v.y; xv[k][6] = v.z; xv[k][7] = v.w;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; ++i) xv[k][i] = 0.f;
-            }
-            mx = fmaxf(mx, finite_max8(xv[k]));
-        }
-        mg_barrier();  // the previous chunk's fragments and maxima are consumed
-        if (tid < kMgTok) tok_max[(ch + 1) & 1][tid] = 0u;
-        if (mx > 0.f) atomicMax(&tmax[tl], __float_as_uint(mx));
-        mg_barrier();
-        {
-            const int e = norm_exp(__uint_as_float(tmax[tl]));
-            uint4* fp = frag + xg * 64 + (tl >> 3) * 16 + 2 * (tl & 7);
-#pragma unroll
-            for (int k = 0; k < XI; ++k) {
-                const int st = xs0 + 2 * k;
-                if (st < ns) {
-                    uint4 hi, lo;
-                    split8(xv[k], e, hi, lo);
-                    fp[st * 256] = hi;
-                    fp[st * 256 + 1] = lo;
-                }
-            }
-        }
-        mg_barrier();
-        // the exponents of this lane's D rows (tokens 2g and 2g + 1 of each sub-tile)
-        int te[kMgSub][2];
-#pragma unroll
-        for (int s = 0; s < kMgSub; ++s) {
-            te[s][0] = norm_exp(__uint_as_float(tmax[s * 8 + 2 * g]));
-            te[s][1] = norm_exp(__uint_as_float(tmax[s * 8 + 2 * g + 1]));
-        }
-
         for (int b = b0; b < b1; ++b) {
-            // next block (of this chunk or the next), clamped to the last block
             const int bn = b + 1 < nblk ? b + 1 : nblk - 1;
-            F::template load<AL>(rp0 + (size_t)bn * F::BPB, g, na);
-            F::template load<AL>(rp1 + (size_t)bn * F::BPB, g, nb);
-
-            f4v D[kMgSub][2][F::NACC];
 #pragma unroll
-            for (int s = 0; s < kMgSub; ++s)
+            for (int i = 0; i < NT; ++i) F::template load<AL, false, UA>(rp[i] + (size_t)bn * F::BPB, g, na[i]);
+            // keep the next block's loads here, a whole block ahead of their use
+            __builtin_amdgcn_sched_barrier(0);
+            typename MxPreOf<F>::type pre[NT];
 #pragma unroll
-                for (int p = 0; p < F::NACC; ++p) D[s][0][p] = D[s][1][p] = f4v{0.f, 0.f, 0.f, 0.f};
-            const uint4* fb = frag + (size_t)(b - b0) * F::STEPS * 4 * 64;
-            typename MxPreOf<F>::type pa, pb;
-            mx_prep<F>(ca, g, pa);
-            mx_prep<F>(cb, g, pb);
+            for (int i = 0; i < NT; ++i) mx_prep<F>(ca[i], g, pre[i]);
+            const uint4* fb = ab + (b - b0) * XPB * TF * 64;
+            f4v D[TF][NT][NA];
 #pragma unroll
             for (int st = 0; st < F::STEPS; ++st) {
-                uint32_t ba[F::NACC][4], bb[F::NACC][4];
-                mx_frag<F>(ca, pa, st, g, ba);
-                mx_frag<F>(cb, pb, st, g, bb);
+                uint32_t B[NT][NA][4];
 #pragma unroll
-                for (int s = 0; s < kMgSub; ++s) {
-                    const uint4 av = fb[(st * 4 + g) * 64 + s * 16 + n];
-                    const uint32_t aw[4] = {av.x, av.y, av.z, av.w};
-                    const h8v A = __builtin_bit_cast(h8v, aw);
+                for (int i = 0; i < NT; ++i) {
+                    if constexpr (MS) F::frag_main(ca[i], pre[i], st, B[i][0]);
+                    else mx_frag<F>(ca[i], pre[i], st, g, B[i]);
+                }
+                // all of the step's token fragments requested at once
+                uint4 Av[TF];
 #pragma unroll
-                    for (int p = 0; p < F::NACC; ++p) {
-                        D[s][0][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8v, ba[p]),
-                                                                           D[s][0][p], 0, 0, 0);
-                        D[s][1][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, __builtin_bit_cast(h8v, bb[p]),
-                                                                           D[s][1][p], 0, 0, 0);
-                    }
+                for (int f = 0; f < TF; ++f) Av[f] = fb[(st * TF + f) * 64];
+#pragma unroll
+                for (int f = 0; f < TF; ++f) {
+                    const h8v A = as_h8(Av[f]);
+#pragma unroll
+                    for (int i = 0; i < NT; ++i)
+#pragma unroll
+                        for (int p = 0; p < NA; ++p)
+                            D[f][i][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                A, __builtin_bit_cast(h8v, B[i][p]),
+                                st == 0 ? f4v{0.f, 0.f, 0.f, 0.f} : D[f][i][p], 0, 0, 0);
                 }
             }
+            if constexpr (MS) {
+                // acc += d D - dmin (sum_j 32 m_j * 2^-5 S_j)
+                float dm[NT];
+                uint32_t Bm[NT][4];
 #pragma unroll
-            for (int s = 0; s < kMgSub; ++s) {
+                for (int i = 0; i < NT; ++i) {
+                    const float d = F::dscale(ca[i]);
+                    dm[i] = -F::mscale(ca[i]);
+                    F::min_frag(ca[i], g, Bm[i]);
 #pragma unroll
-                for (int p = 0; p < F::NACC; ++p) {
+                    for (int f = 0; f < TF; ++f) {
+                        f4v& q = acc[f][i];
 #pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        f4v& q = D[s][h][p];
-                        q[0] = __builtin_amdgcn_ldexpf(q[0], te[s][0]);
-                        q[1] = __builtin_amdgcn_ldexpf(q[1], te[s][0]);
-                        q[2] = __builtin_amdgcn_ldexpf(q[2], te[s][1]);
-                        q[3] = __builtin_amdgcn_ldexpf(q[3], te[s][1]);
+                        for (int k = 0; k < 4; ++k) q[k] = fmaf(d, D[f][i][0][k], q[k]);
                     }
                 }
-                F::epi(ca, D[s][0], acc[s][0]);
-                F::epi(cb, D[s][1], acc[s][1]);
+#pragma unroll
+                for (int f = 0; f < TF; ++f) {
+                    const h8v A = as_h8(fb[(F::STEPS * TF + f) * 64]);
+#pragma unroll
+                    for (int i = 0; i < NT; ++i)
+                        D[f][i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            A, __builtin_bit_cast(h8v, Bm[i]), f4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                }
+#pragma unroll
+                for (int f = 0; f < TF; ++f)
+#pragma unroll
+                    for (int i = 0; i < NT; ++i) {
+                        f4v& q = acc[f][i];
+#pragma unroll
+                        for (int k = 0; k < 4; ++k) q[k] = fmaf(dm[i], D[f][i][0][k], q[k]);
+                    }
+            } else {
+#pragma unroll
+                for (int f = 0; f < TF; ++f)
+#pragma unroll
+                    for (int i = 0; i < NT; ++i) F::epi(ca[i], D[f][i], acc[f][i]);
             }
-            ca = na;
-            cb = nb;
+#pragma unroll
+            for (int i = 0; i < NT; ++i) ca[i] = na[i];
         }
     }
 
-    // D rows 4g..4g+3 = (token 2g: hi, lo), (token 2g + 1: hi, lo) of each sub-tile
+    // D rows 4g..4g+3 = (token 2g: hi, lo), (token 2g + 1: hi, lo) of each fragment
 #pragma unroll
-    for (int s = 0; s < kMgSub; ++s) {
-        const int t0 = tok0 + s * 8 + 2 * g;
+    for (int f = 0; f < TF; ++f) {
+        const int t0 = (tt * TF + f) * 8 + 2 * g;
+        const int e0 = t0 < a.batch ? a.texp[t0] : 0, e1 = t0 + 1 < a.batch ? a.texp[t0 + 1] : 0;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const long long row = h ? r1 : r0;
-            if (row >= a.rows) continue;
-            const f4v v = acc[s][h];
-            if (t0 < a.batch) a.Y[(unsigned long long)t0 * a.ldy + row] = v[0] + v[1];
-            if (t0 + 1 < a.batch) a.Y[(unsigned long long)(t0 + 1) * a.ldy + row] = v[2] + v[3];
+        for (int i = 0; i < NT; ++i) {
+            const long long row = rbase + 16 * i;
+            if (row >= rows) continue;
+            const f4v v = acc[f][i];
+            if (t0 < a.batch) Y[(unsigned long long)t0 * ldy + row] = __builtin_amdgcn_ldexpf(v[0] + v[1], e0);
+            if (t0 + 1 < a.batch)
+                Y[(unsigned long long)(t0 + 1) * ldy + row] = __builtin_amdgcn_ldexpf(v[2] + v[3], e1);
         }
     }
 }
 
+// ---------------------------------------------------------------- launch
+// Activation fragments and exponents, one per device, grown on demand (never
+// during stream capture; a replaced block stays allocated for graphs captured
+// before).  Launches on one device must be ordered on one stream.
+struct MgWorkspace {
+    void* block = nullptr;
+    size_t cap = 0;  // bytes
+};
+static MgWorkspace g_mg_ws[64];
+
 template <int T, bool AL>
-static hipError_t mg_launch_t(const MgArgs& a, hipStream_t s, hipEvent_t e0, hipEvent_t e1) {
-    const unsigned wgs = (unsigned)((long long)a.row_tiles * a.tok_tiles);
-    if (e0 || e1)
-        hipExtLaunchKernelGGL((mg_kernel<T, AL>), dim3(wgs), dim3(256), 0, s, e0, e1, 0, a);
+static hipError_t mg_launch_t(MgArgs& a, const float* X, unsigned long long ldx, hipStream_t s, hipEvent_t e0,
+                              hipEvent_t e1) {
+    using F = Mx<T>;
+    const int nsteps = a.cols / 32, nblk = a.cols / F::BS;
+    const size_t frag_bytes = (size_t)nblk * mg_xs_per_block<F>() * a.Fp * 1024;
+    const size_t need = frag_bytes + ((size_t)a.batch * sizeof(int) + 255) / 256 * 256;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    MgWorkspace& ws = g_mg_ws[dev];
+    if (need > ws.cap && (e = workspace_grow(&ws.block, &ws.cap, need, false, s)) != hipSuccess) return e;
+    uint4* XF = static_cast<uint4*>(ws.block);
+    int* texp = reinterpret_cast<int*>(static_cast<uint8_t*>(ws.block) + frag_bytes);
+    a.XF = XF;
+    a.texp = texp;
+    const dim3 gexp(a.batch), gfrag((unsigned)((long long)a.Fp * ((nsteps + 7) / 8)));
+    if (e0)
+        hipExtLaunchKernelGGL(mg_exp_kernel, gexp, dim3(256), 0, s, e0, nullptr, 0, X, ldx, a.cols, texp);
     else
-        hipLaunchKernelGGL((mg_kernel<T, AL>), dim3(wgs), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(mg_exp_kernel, gexp, dim3(256), 0, s, X, ldx, a.cols, texp);
+    hipLaunchKernelGGL((mg_frag_kernel<T>), gfrag, dim3(256), 0, s, X, ldx, a.cols, a.batch, (const int*)texp, XF,
+                       a.Fp);
+    const unsigned wgs = (unsigned)((long long)a.row_tiles * a.tok_tiles);
+    if (e1)
+        hipExtLaunchKernelGGL((mg_kernel<T, AL>), dim3(wgs), dim3(kMgWaves * 64), 0, s, nullptr, e1, 0, a);
+    else
+        hipLaunchKernelGGL((mg_kernel<T, AL>), dim3(wgs), dim3(kMgWaves * 64), 0, s, a);
     return hipGetLastError();
 }
 
-int mg_launch(int type, const MatvecArgs& m, size_t batch, bool al, hipStream_t stream, hipEvent_t start,
-              hipEvent_t stop) {
-    const TypeGeo g = type_geo(type);
-    MgArgs a;
-    a.W = static_cast<const uint8_t*>(m.w);
-    a.row_bytes = m.cols / g.bs * g.bpb;
-    a.X = m.x;
-    a.ldx = m.ldx;
-    a.Y = m.y;
-    a.ldy = m.ldy;
-    a.rows = (int)m.rows;
-    a.cols = (int)m.cols;
+template <int T>
+static int mg_tokens_per_tile() { return 8 * mg_tf<Mx<T>>(); }
+
+// One launch set per run of consecutive matrices with the same activations
+// and columns (at most kMgMaxMats each).
+int mg_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, bool al, hipStream_t stream,
+                    hipEvent_t start, hipEvent_t stop) {
+    const TypeGeo geo = type_geo(type);
     if (batch > 0x7FFFFFFF) return -2;
-    a.batch = (int)batch;
-    a.row_tiles = (int)((m.rows + kMgRows - 1) / kMgRows);
-    a.tok_tiles = (int)((batch + kMgTok - 1) / kMgTok);
-    if ((long long)a.row_tiles * a.tok_tiles > 0x7FFFFFFFLL) return -2;
-    hipError_t e = hipSuccess;
-#define PYRITE_CASE(T)                                                                         \
-    case T:                                                                                  \
-        e = (al && Geo<T>::bpb % 4 == 0) ? mg_launch_t<T, (Geo<T>::bpb % 4 == 0)>(a, stream, start, stop) \
-                                         : mg_launch_t<T, false>(a, stream, start, stop);    \
-        break;
+    int tok = 0;
+#define PYRITE_CASE(T) case T: tok = mg_tokens_per_tile<T>(); break;
     switch (type) {
         PYRITE_CASE(T_Q4_0) PYRITE_CASE(T_Q4_1) PYRITE_CASE(T_Q5_0) PYRITE_CASE(T_Q5_1)
         PYRITE_CASE(T_Q8_0) PYRITE_CASE(T_Q8_1) PYRITE_CASE(T_Q2_K) PYRITE_CASE(T_Q3_K)
@@ -241,7 +440,52 @@ int mg_launch(int type, const MatvecArgs& m, size_t batch, bool al, hipStream_t 
     default: return -1;
     }
 #undef PYRITE_CASE
-    return e == hipSuccess ? 0 : -4;
+    size_t i = 0;
+    while (i < n) {
+        size_t j = i + 1;
+        while (j < n && j - i < (size_t)kMgMaxMats && mats[j].x == mats[i].x && mats[j].ldx == mats[i].ldx &&
+               mats[j].cols == mats[i].cols)
+            ++j;
+        MgArgs a{};
+        a.nmat = (int)(j - i);
+        long long tiles = 0;
+        for (size_t k = i; k < j; ++k) {
+            MgMat& d = a.m[k - i];
+            d.W = static_cast<const uint8_t*>(mats[k].w);
+            d.row_bytes = mats[k].cols / geo.bs * geo.bpb;
+            d.Y = mats[k].y;
+            d.ldy = mats[k].ldy;
+            d.rows = (int)mats[k].rows;
+            d.tile0 = (int)tiles;
+            tiles += (long long)((mats[k].rows + kMgRows - 1) / kMgRows);
+        }
+        a.cols = (int)mats[i].cols;
+        a.batch = (int)batch;
+        a.row_tiles = (int)tiles;
+        a.tok_tiles = (int)((batch + tok - 1) / tok);
+        a.Fp = a.tok_tiles * (tok / 8);
+        if (tiles * a.tok_tiles > 0x7FFFFFFFLL || (long long)a.Fp * ((a.cols / 32 + 7) / 8) > 0x7FFFFFFFLL)
+            return -2;
+        hipEvent_t e0 = i == 0 ? start : nullptr, e1 = j == n ? stop : nullptr;
+        hipError_t e = hipSuccess;
+#define PYRITE_CASE(T)                                                                                     \
+    case T:                                                                                                \
+        e = (al && Geo<T>::bpb % 4 == 0) ? mg_launch_t<T, (Geo<T>::bpb % 4 == 0)>(a, mats[i].x, mats[i].ldx, \
+                                                                                 stream, e0, e1)           \
+                                         : mg_launch_t<T, false>(a, mats[i].x, mats[i].ldx, stream, e0, e1); \
+        break;
+        switch (type) {
+            PYRITE_CASE(T_Q4_0) PYRITE_CASE(T_Q4_1) PYRITE_CASE(T_Q5_0) PYRITE_CASE(T_Q5_1)
+            PYRITE_CASE(T_Q8_0) PYRITE_CASE(T_Q8_1) PYRITE_CASE(T_Q2_K) PYRITE_CASE(T_Q3_K)
+            PYRITE_CASE(T_Q4_K) PYRITE_CASE(T_Q5_K) PYRITE_CASE(T_Q6_K) PYRITE_CASE(T_IQ4_NL)
+            PYRITE_CASE(T_IQ4_XS)
+        default: return -1;
+        }
+#undef PYRITE_CASE
+        if (e != hipSuccess) return -4;
+        i = j;
+    }
+    return 0;
 }
 
 }  // namespace pyrite

@@ -172,17 +172,20 @@ __device__ __forceinline__ void gl_span(const uint8_t* b, int off, uint32_t (&w)
 #pragma unroll
     for (int k = 0; k < N; ++k) w[k] = __builtin_amdgcn_alignbyte(t[k + 1], t[k], s);
 }
-// the span reader of a format's load: global memory or LDS (L)
-template <int NB, bool AL, bool L>
+// the span reader of a format's load: global memory or LDS (L); unaligned
+// global spans as dword-aligned loads realigned by v_alignbyte_b32, or (UA)
+// as loads at the span's own byte address
+template <int NB, bool AL, bool L, bool UA = false>
 __device__ __forceinline__ void mx_span(const uint8_t* b, int off, uint32_t (&w)[(NB + 3) / 4]) {
     if constexpr (AL) ld_span<NB, AL>(b + off, w);
     else if constexpr (L) lds_span<NB>(b, off, w);
+    else if constexpr (UA) ld_span<NB, false, true>(b + off, w);
     else gl_span<NB>(b, off, w);
 }
-template <bool AL, bool L>
+template <bool AL, bool L, bool UA = false>
 __device__ __forceinline__ void mx_ld8(const uint8_t* b, int off, uint32_t& x, uint32_t& y) {
     uint32_t w[2];
-    mx_span<8, AL, L>(b, off, w);
+    mx_span<8, AL, L, UA>(b, off, w);
     x = w[0];
     y = w[1];
 }
@@ -251,10 +254,10 @@ template <> struct Mx<T_Q4_K> {
     struct Raw { uint32_t hd[4]; uint32_t q[8]; };
     // packed (s, s), (-1024 s, -1024 s) and (m, m) halves of sub-blocks 2g, 2g + 1
     struct Pre { uint32_t S[2], O[2], M[2]; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        mx_span<16, AL, L>(b, 0, r.hd);
-        mx_span<32, AL, L>(b, 16 + 32 * g, r.q);
+        mx_span<16, AL, L, UA>(b, 0, r.hd);
+        mx_span<32, AL, L, UA>(b, 16 + 32 * g, r.q);
     }
     // scale and min of sub-block j, any j in 0..7 (get_scale_min_k4, native.c:52-61)
     __device__ __forceinline__ static void k4_scale_min_rt(const uint32_t (&hd)[4], int j, uint32_t& a, uint32_t& m) {
@@ -303,18 +306,47 @@ template <> struct Mx<T_Q4_K> {
         const float d = half_bits_to_float(r.hd[0]), dmin = half_bits_to_float(r.hd[0] >> 16);
         acc += d * D[0] - dmin * D[1];
     }
+    // Dequant-GEMM form (mg.hip): the min term dmin * sum_j m_j S_j, with S_j
+    // the activations' sum over sub-block j, is one MFMA per block against
+    // staged sub-block sums, so the per-step fragments carry the codes only.
+    static constexpr bool MINSUM = true;
+    __device__ __forceinline__ static void frag_main(const Raw& r, const Pre& p, int s, uint32_t (&b)[4]) {
+        const int h = s >> 2, k = s & 3;
+        uint32_t x0 = r.q[2 * k], x1 = r.q[2 * k + 1];
+        if (h) { x0 >>= 4; x1 >>= 4; }
+        x0 &= 0x0F0F0F0Fu;
+        x1 &= 0x0F0F0F0Fu;
+        b[0] = pk_fma(bias_lo(x0), p.S[h], p.O[h]);
+        b[1] = pk_fma(bias_hi(x0), p.S[h], p.O[h]);
+        b[2] = pk_fma(bias_lo(x1), p.S[h], p.O[h]);
+        b[3] = pk_fma(bias_hi(x1), p.S[h], p.O[h]);
+    }
+    // B of the min MFMA: K-slot j < 8 (lane group 0) holds 32 m_j (exact:
+    // at most 2016), the other K-slots 0.  The staged sums carry 2^-5.
+    __device__ __forceinline__ static void min_frag(const Raw& r, int g, uint32_t (&b)[4]) {
+        const uint32_t m03 = r.hd[2] & 0x3F3F3F3Fu;
+        const uint32_t m47 = ((r.hd[3] >> 4) & 0x0F0F0F0Fu) | ((r.hd[2] >> 2) & 0x30303030u);
+        const float sc = g == 0 ? 32.f : 0.f;
+        const uint32_t S = splat_h(sc), O = splat_h(-1024.f * sc);
+        b[0] = pk_fma(bias_lo(m03), S, O);
+        b[1] = pk_fma(bias_hi(m03), S, O);
+        b[2] = pk_fma(bias_lo(m47), S, O);
+        b[3] = pk_fma(bias_hi(m47), S, O);
+    }
+    __device__ __forceinline__ static float dscale(const Raw& r) { return half_bits_to_float(r.hd[0]); }
+    __device__ __forceinline__ static float mscale(const Raw& r) { return half_bits_to_float(r.hd[0] >> 16); }
 };
 
 // Q5_K: as Q4_K with a fifth bit, qh[l] bit j (native.c:410-437).
 template <> struct Mx<T_Q5_K> {
     static constexpr int BS = 256, BPB = 176, STEPS = 8, NACC = 2;
     struct Raw { uint32_t hd[4]; uint32_t h[2]; uint32_t q[4][2]; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        mx_span<16, AL, L>(b, 0, r.hd);
-        mx_ld8<AL, L>(b, 16 + 8 * g, r.h[0], r.h[1]);
+        mx_span<16, AL, L, UA>(b, 0, r.hd);
+        mx_ld8<AL, L, UA>(b, 16 + 8 * g, r.h[0], r.h[1]);
 #pragma unroll
-        for (int c = 0; c < 4; ++c) mx_ld8<AL, L>(b, 48 + 32 * c + 8 * g, r.q[c][0], r.q[c][1]);
+        for (int c = 0; c < 4; ++c) mx_ld8<AL, L, UA>(b, 48 + 32 * c + 8 * g, r.q[c][0], r.q[c][1]);
     }
     __device__ __forceinline__ static void frag(const Raw& r, int j, int, uint32_t (&b)[2][4]) {
         const int c = j >> 1;
@@ -340,15 +372,15 @@ template <> struct Mx<T_Q5_K> {
 template <> struct Mx<T_Q6_K> {
     static constexpr int BS = 256, BPB = 210, STEPS = 8, NACC = 2;
     struct Raw { uint32_t ql[4][2]; uint32_t qh[2][2]; uint32_t sc[4]; uint32_t d; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
 #pragma unroll
-        for (int k = 0; k < 4; ++k) mx_ld8<AL, L>(b, 64 * (k >> 1) + 32 * (k & 1) + 8 * g, r.ql[k][0], r.ql[k][1]);
+        for (int k = 0; k < 4; ++k) mx_ld8<AL, L, UA>(b, 64 * (k >> 1) + 32 * (k & 1) + 8 * g, r.ql[k][0], r.ql[k][1]);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) mx_ld8<AL, L>(b, 128 + 32 * h + 8 * g, r.qh[h][0], r.qh[h][1]);
-        mx_span<16, AL, L>(b, 192, r.sc);
+        for (int h = 0; h < 2; ++h) mx_ld8<AL, L, UA>(b, 128 + 32 * h + 8 * g, r.qh[h][0], r.qh[h][1]);
+        mx_span<16, AL, L, UA>(b, 192, r.sc);
         uint32_t dd[1];
-        mx_span<2, AL, L>(b, 208, dd);
+        mx_span<2, AL, L, UA>(b, 208, dd);
         r.d = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int s, int g, uint32_t (&b)[2][4]) {
@@ -376,14 +408,14 @@ template <> struct Mx<T_Q6_K> {
 template <> struct Mx<T_Q3_K> {
     static constexpr int BS = 256, BPB = 110, STEPS = 8, NACC = 1;
     struct Raw { uint32_t qs[2][2]; uint32_t hm[2]; uint32_t sc[3]; uint32_t d; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) mx_ld8<AL, L>(b, 32 + 32 * h + 8 * g, r.qs[h][0], r.qs[h][1]);
-        mx_ld8<AL, L>(b, 8 * g, r.hm[0], r.hm[1]);
-        mx_span<12, AL, L>(b, 96, r.sc);
+        for (int h = 0; h < 2; ++h) mx_ld8<AL, L, UA>(b, 32 + 32 * h + 8 * g, r.qs[h][0], r.qs[h][1]);
+        mx_ld8<AL, L, UA>(b, 8 * g, r.hm[0], r.hm[1]);
+        mx_span<12, AL, L, UA>(b, 96, r.sc);
         uint32_t dd[1];
-        mx_span<2, AL, L>(b, 108, dd);
+        mx_span<2, AL, L, UA>(b, 108, dd);
         r.d = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int s, int g, uint32_t (&b)[1][4]) {
@@ -410,13 +442,13 @@ template <> struct Mx<T_Q3_K> {
 template <> struct Mx<T_Q2_K> {
     static constexpr int BS = 256, BPB = 84, STEPS = 8, NACC = 2;
     struct Raw { uint32_t qs[2][2]; uint32_t sc[4]; uint32_t dd; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) mx_ld8<AL, L>(b, 16 + 32 * h + 8 * g, r.qs[h][0], r.qs[h][1]);
-        mx_span<16, AL, L>(b, 0, r.sc);
+        for (int h = 0; h < 2; ++h) mx_ld8<AL, L, UA>(b, 16 + 32 * h + 8 * g, r.qs[h][0], r.qs[h][1]);
+        mx_span<16, AL, L, UA>(b, 0, r.sc);
         uint32_t dd[1];
-        mx_span<4, AL, L>(b, 80, dd);
+        mx_span<4, AL, L, UA>(b, 80, dd);
         r.dd = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int s, int g, uint32_t (&b)[2][4]) {
@@ -439,11 +471,11 @@ template <> struct Mx<T_Q2_K> {
 template <> struct Mx<T_IQ4_XS> {
     static constexpr int BS = 256, BPB = 136, STEPS = 8, NACC = 2;
     struct Raw { uint32_t hd[2]; uint32_t q[8][2]; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        mx_span<8, AL, L>(b, 0, r.hd);
+        mx_span<8, AL, L, UA>(b, 0, r.hd);
 #pragma unroll
-        for (int ib = 0; ib < 8; ++ib) mx_ld8<AL, L>(b, 8 + 16 * ib + 8 * (g & 1), r.q[ib][0], r.q[ib][1]);
+        for (int ib = 0; ib < 8; ++ib) mx_ld8<AL, L, UA>(b, 8 + 16 * ib + 8 * (g & 1), r.q[ib][0], r.q[ib][1]);
     }
     __device__ __forceinline__ static void frag(const Raw& r, int ib, int g, uint32_t (&b)[2][4]) {
         uint32_t x0 = r.q[ib][0], x1 = r.q[ib][1];
@@ -463,9 +495,9 @@ template <> struct Mx<T_IQ4_XS> {
 
 // 32-element blocks: one step per block; lane group g owns columns 8g..8g+7,
 // the low nibbles of qs[8g..] for g < 2 and the high nibbles of qs[8(g-2)..].
-template <int OFF, int NB, bool AL, bool L>
+template <int OFF, int NB, bool AL, bool L, bool UA = false>
 __device__ __forceinline__ void ld_nib8(const uint8_t* b, int g, uint32_t& x0, uint32_t& x1) {
-    mx_ld8<AL, L>(b, OFF + 8 * (g & 1), x0, x1);
+    mx_ld8<AL, L, UA>(b, OFF + 8 * (g & 1), x0, x1);
     if (g & 2) { x0 >>= 4; x1 >>= 4; }
     x0 &= 0x0F0F0F0Fu;
     x1 &= 0x0F0F0F0Fu;
@@ -475,11 +507,11 @@ __device__ __forceinline__ void ld_nib8(const uint8_t* b, int g, uint32_t& x0, u
 template <> struct Mx<T_Q4_0> {
     static constexpr int BS = 32, BPB = 18, STEPS = 1, NACC = 1;
     struct Raw { uint32_t x0, x1, d; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_nib8<2, 18, AL, L>(b, g, r.x0, r.x1);
+        ld_nib8<2, 18, AL, L, UA>(b, g, r.x0, r.x1);
         uint32_t dd[1];
-        mx_span<2, AL, L>(b, 0, dd);
+        mx_span<2, AL, L, UA>(b, 0, dd);
         r.d = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int, int, uint32_t (&b)[1][4]) {
@@ -494,11 +526,11 @@ template <> struct Mx<T_Q4_0> {
 template <> struct Mx<T_IQ4_NL> {
     static constexpr int BS = 32, BPB = 18, STEPS = 1, NACC = 1;
     struct Raw { uint32_t x0, x1, d; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_nib8<2, 18, AL, L>(b, g, r.x0, r.x1);
+        ld_nib8<2, 18, AL, L, UA>(b, g, r.x0, r.x1);
         uint32_t dd[1];
-        mx_span<2, AL, L>(b, 0, dd);
+        mx_span<2, AL, L, UA>(b, 0, dd);
         r.d = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int, int, uint32_t (&b)[1][4]) {
@@ -513,11 +545,11 @@ template <> struct Mx<T_IQ4_NL> {
 template <> struct Mx<T_Q4_1> {
     static constexpr int BS = 32, BPB = 20, STEPS = 1, NACC = 2;
     struct Raw { uint32_t x0, x1, dm; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_nib8<4, 20, AL, L>(b, g, r.x0, r.x1);
+        ld_nib8<4, 20, AL, L, UA>(b, g, r.x0, r.x1);
         uint32_t dd[1];
-        mx_span<4, AL, L>(b, 0, dd);
+        mx_span<4, AL, L, UA>(b, 0, dd);
         r.dm = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int, int, uint32_t (&b)[2][4]) {
@@ -540,11 +572,11 @@ __device__ __forceinline__ void q5_high(uint32_t qh, int g, uint32_t& x0, uint32
 template <> struct Mx<T_Q5_0> {
     static constexpr int BS = 32, BPB = 22, STEPS = 1, NACC = 1;
     struct Raw { uint32_t x0, x1, d; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_nib8<6, 22, AL, L>(b, g, r.x0, r.x1);
+        ld_nib8<6, 22, AL, L, UA>(b, g, r.x0, r.x1);
         uint32_t w[2];
-        mx_span<6, AL, L>(b, 0, w);
+        mx_span<6, AL, L, UA>(b, 0, w);
         r.d = w[0];
         q5_high(__builtin_amdgcn_alignbyte(w[1], w[0], 2u), g, r.x0, r.x1);
     }
@@ -560,11 +592,11 @@ template <> struct Mx<T_Q5_0> {
 template <> struct Mx<T_Q5_1> {
     static constexpr int BS = 32, BPB = 24, STEPS = 1, NACC = 2;
     struct Raw { uint32_t x0, x1, dm; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        ld_nib8<8, 24, AL, L>(b, g, r.x0, r.x1);
+        ld_nib8<8, 24, AL, L, UA>(b, g, r.x0, r.x1);
         uint32_t w[2];
-        mx_span<8, AL, L>(b, 0, w);
+        mx_span<8, AL, L, UA>(b, 0, w);
         r.dm = w[0];
         q5_high(w[1], g, r.x0, r.x1);
     }
@@ -583,11 +615,11 @@ template <int OFF, int NB>
 struct MxQ8 {
     static constexpr int BS = 32, BPB = NB, STEPS = 1, NACC = 1;
     struct Raw { uint32_t x0, x1, d; };
-    template <bool AL, bool L = false>
+    template <bool AL, bool L = false, bool UA = false>
     __device__ __forceinline__ static void load(const uint8_t* b, int g, Raw& r) {
-        mx_ld8<AL, L>(b, OFF + 8 * g, r.x0, r.x1);
+        mx_ld8<AL, L, UA>(b, OFF + 8 * g, r.x0, r.x1);
         uint32_t dd[1];
-        mx_span<2, AL, L>(b, 0, dd);
+        mx_span<2, AL, L, UA>(b, 0, dd);
         r.d = dd[0];
     }
     __device__ __forceinline__ static void frag(const Raw& r, int, int, uint32_t (&b)[1][4]) {
