@@ -55,10 +55,12 @@ template <class F> struct MgMinSum<F, std::void_t<decltype(F::MINSUM)>> : std::b
 template <class F>
 constexpr int mg_xs_per_block() { return F::STEPS + (MgMinSum<F>::value ? 1 : 0); }
 
-// 8-token fragments per workgroup: 8 for MINSUM formats (one accumulator per
-// block), 4 for the others (two), so that a wave fits in 256 registers
+// 8-token fragments per workgroup: up to 8 for MINSUM formats (one
+// accumulator per block), 4 for the others (two), so that a wave fits in 256
+// registers.  Launches whose 32-token workgroups fit in one pass over the
+// CUs take 4.
 template <class F>
-constexpr int mg_tf() { return MgMinSum<F>::value ? 8 : 4; }
+constexpr int mg_tf_max() { return MgMinSum<F>::value ? 8 : 4; }
 
 struct MgMat {
     const uint8_t* W;
@@ -199,19 +201,27 @@ __device__ __forceinline__ h8v as_h8(const uint4 v) {
     return __builtin_bit_cast(h8v, w);
 }
 
-template <int T, bool AL>
+template <int T, bool AL, int TF>
 __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
     using F = Mx<T>;
     constexpr bool MS = MgMinSum<F>::value;
-    constexpr int NT = kMgWaveTiles, TF = mg_tf<F>();
+    constexpr int NT = kMgWaveTiles;
     constexpr int NA = MS ? 1 : F::NACC;                                 // accumulators per block
     constexpr int BPC = F::STEPS >= kMgChunk ? 1 : kMgChunk / F::STEPS;  // blocks per chunk
     constexpr int XPB = mg_xs_per_block<F>();
     constexpr int CX = BPC * XPB;  // fragment steps per chunk
     constexpr int CF = CX * TF;    // fragments per chunk
-    // unaligned super-blocks: loads at the spans' own byte addresses
+    // Super-block formats other than MINSUM ones (unaligned 84- to 210-byte
+    // blocks): each wave copies its 32 rows' next block into its own LDS
+    // region with aligned 16-byte direct loads (the 16-byte pieces that
+    // overlap the block: never past the page of its last byte), and its
+    // lanes read their spans from there.  Other formats load their spans
+    // straight into registers, one block ahead.
+    constexpr bool WL = F::BS == 256 && !MS;
+    constexpr int WP = WL ? (15 + F::BPB + 4 + 15) / 16 : 1;  // 16-byte pieces per row region
     constexpr bool UA = !AL && F::BS == 256;
     __shared__ uint4 abuf[2][CF * 64];
+    __shared__ uint4 wbuf[WL ? kMgWaves * 16 * NT * WP : 1];
 
     // XCD-aware order: workgroup b runs on XCD b % 8; logical tile L counts
     // each XCD's workgroups contiguously, so the token tiles of a row tile
@@ -264,9 +274,32 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
         }
     };
 
-    typename F::Raw ca[NT], na[NT];
+    // WL: this wave's row region; lane (row q / WP, piece q % WP) of copy k, q = 64 k + lane
+    uint4* wreg = wbuf + w * 16 * NT * WP;
+    auto wstage = [&](int blk) {
 #pragma unroll
-    for (int i = 0; i < NT; ++i) F::template load<AL, false, UA>(rp[i], g, ca[i]);
+        for (int k = 0; k < (16 * NT * WP + 63) / 64; ++k) {
+            const int q = 64 * k + lane, r = q / WP, pc = q - r * WP;
+            const long long row = rbase - n + r;
+            const uint8_t* bp = W + (row < rows ? row : rows - 1) * row_bytes + (size_t)blk * F::BPB;
+            const uint8_t* a0 = bp - (reinterpret_cast<uintptr_t>(bp) & 15u);
+            if (r < 16 * NT && a0 + 16 * pc < bp + F::BPB)
+                lds_load_1k(reinterpret_cast<const uint4*>(a0) + pc, wreg + 64 * k);
+        }
+    };
+    // WL: the block's bytes of tile i's row in the wave's region
+    auto wrow = [&](int i, int blk) {
+        const uintptr_t o = reinterpret_cast<uintptr_t>(rp[i] + (size_t)blk * F::BPB) & 15u;
+        return reinterpret_cast<const uint8_t*>(wreg + (16 * i + n) * WP) + o;
+    };
+
+    typename F::Raw ca[NT], na[NT];
+    if constexpr (WL) {
+        wstage(0);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NT; ++i) F::template load<AL, false, UA>(rp[i], g, ca[i]);
+    }
     stage(0, 0);
 
     f4v acc[TF][NT];
@@ -286,8 +319,18 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
         const int b1 = b0 + BPC < nblk ? b0 + BPC : nblk;
         for (int b = b0; b < b1; ++b) {
             const int bn = b + 1 < nblk ? b + 1 : nblk - 1;
+            if constexpr (WL) {
+                // this block's spans out of the wave's region (landed: the
+                // chunk began with vmcnt(0)), then the next block into it
 #pragma unroll
-            for (int i = 0; i < NT; ++i) F::template load<AL, false, UA>(rp[i] + (size_t)bn * F::BPB, g, na[i]);
+                for (int i = 0; i < NT; ++i) F::template load<false, true>(wrow(i, b), g, ca[i]);
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                if (b + 1 < nblk) wstage(b + 1);
+            } else {
+#pragma unroll
+                for (int i = 0; i < NT; ++i)
+                    F::template load<AL, false, UA>(rp[i] + (size_t)bn * F::BPB, g, na[i]);
+            }
             // keep the next block's loads here, a whole block ahead of their use
             __builtin_amdgcn_sched_barrier(0);
             typename MxPreOf<F>::type pre[NT];
@@ -357,8 +400,10 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
 #pragma unroll
                     for (int i = 0; i < NT; ++i) F::epi(ca[i], D[f][i], acc[f][i]);
             }
+            if constexpr (!WL) {
 #pragma unroll
-            for (int i = 0; i < NT; ++i) ca[i] = na[i];
+                for (int i = 0; i < NT; ++i) ca[i] = na[i];
+            }
         }
     }
 
@@ -389,7 +434,7 @@ struct MgWorkspace {
 };
 static MgWorkspace g_mg_ws[64];
 
-template <int T, bool AL>
+template <int T, bool AL, int TF>
 static hipError_t mg_launch_t(MgArgs& a, const float* X, unsigned long long ldx, hipStream_t s, hipEvent_t e0,
                               hipEvent_t e1) {
     using F = Mx<T>;
@@ -415,14 +460,28 @@ static hipError_t mg_launch_t(MgArgs& a, const float* X, unsigned long long ldx,
                        a.Fp);
     const unsigned wgs = (unsigned)((long long)a.row_tiles * a.tok_tiles);
     if (e1)
-        hipExtLaunchKernelGGL((mg_kernel<T, AL>), dim3(wgs), dim3(kMgWaves * 64), 0, s, nullptr, e1, 0, a);
+        hipExtLaunchKernelGGL((mg_kernel<T, AL, TF>), dim3(wgs), dim3(kMgWaves * 64), 0, s, nullptr, e1, 0, a);
     else
-        hipLaunchKernelGGL((mg_kernel<T, AL>), dim3(wgs), dim3(kMgWaves * 64), 0, s, a);
+        hipLaunchKernelGGL((mg_kernel<T, AL, TF>), dim3(wgs), dim3(kMgWaves * 64), 0, s, a);
     return hipGetLastError();
 }
 
+// fragments per workgroup for a launch of `row_tiles` row tiles
 template <int T>
-static int mg_tokens_per_tile() { return 8 * mg_tf<Mx<T>>(); }
+static int mg_tf_for(long long row_tiles, size_t batch) {
+    constexpr int TM = mg_tf_max<Mx<T>>();
+    // 32-token tiles when they still fit in one pass over the 256 CUs
+    if (TM == 8 && row_tiles * (long long)((batch + 31) / 32) <= 256) return 4;
+    return TM;
+}
+
+template <int T, bool AL>
+static hipError_t mg_launch_tf(MgArgs& a, int tf, const float* X, unsigned long long ldx, hipStream_t s,
+                               hipEvent_t e0, hipEvent_t e1) {
+    if constexpr (mg_tf_max<Mx<T>>() == 8)
+        if (tf == 8) return mg_launch_t<T, AL, 8>(a, X, ldx, s, e0, e1);
+    return mg_launch_t<T, AL, 4>(a, X, ldx, s, e0, e1);
+}
 
 // One launch set per run of consecutive matrices with the same activations
 // and columns (at most kMgMaxMats each).
@@ -430,16 +489,6 @@ int mg_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, bo
                     hipEvent_t start, hipEvent_t stop) {
     const TypeGeo geo = type_geo(type);
     if (batch > 0x7FFFFFFF) return -2;
-    int tok = 0;
-#define PYRITE_CASE(T) case T: tok = mg_tokens_per_tile<T>(); break;
-    switch (type) {
-        PYRITE_CASE(T_Q4_0) PYRITE_CASE(T_Q4_1) PYRITE_CASE(T_Q5_0) PYRITE_CASE(T_Q5_1)
-        PYRITE_CASE(T_Q8_0) PYRITE_CASE(T_Q8_1) PYRITE_CASE(T_Q2_K) PYRITE_CASE(T_Q3_K)
-        PYRITE_CASE(T_Q4_K) PYRITE_CASE(T_Q5_K) PYRITE_CASE(T_Q6_K) PYRITE_CASE(T_IQ4_NL)
-        PYRITE_CASE(T_IQ4_XS)
-    default: return -1;
-    }
-#undef PYRITE_CASE
     size_t i = 0;
     while (i < n) {
         size_t j = i + 1;
@@ -459,20 +508,30 @@ int mg_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, bo
             d.tile0 = (int)tiles;
             tiles += (long long)((mats[k].rows + kMgRows - 1) / kMgRows);
         }
+        int tf = 0;
+#define PYRITE_CASE(T) case T: tf = mg_tf_for<T>(tiles, batch); break;
+        switch (type) {
+            PYRITE_CASE(T_Q4_0) PYRITE_CASE(T_Q4_1) PYRITE_CASE(T_Q5_0) PYRITE_CASE(T_Q5_1)
+            PYRITE_CASE(T_Q8_0) PYRITE_CASE(T_Q8_1) PYRITE_CASE(T_Q2_K) PYRITE_CASE(T_Q3_K)
+            PYRITE_CASE(T_Q4_K) PYRITE_CASE(T_Q5_K) PYRITE_CASE(T_Q6_K) PYRITE_CASE(T_IQ4_NL)
+            PYRITE_CASE(T_IQ4_XS)
+        default: return -1;
+        }
+#undef PYRITE_CASE
         a.cols = (int)mats[i].cols;
         a.batch = (int)batch;
         a.row_tiles = (int)tiles;
-        a.tok_tiles = (int)((batch + tok - 1) / tok);
-        a.Fp = a.tok_tiles * (tok / 8);
+        a.tok_tiles = (int)((batch + 8 * tf - 1) / (8 * tf));
+        a.Fp = a.tok_tiles * tf;
         if (tiles * a.tok_tiles > 0x7FFFFFFFLL || (long long)a.Fp * ((a.cols / 32 + 7) / 8) > 0x7FFFFFFFLL)
             return -2;
         hipEvent_t e0 = i == 0 ? start : nullptr, e1 = j == n ? stop : nullptr;
         hipError_t e = hipSuccess;
 #define PYRITE_CASE(T)                                                                                     \
     case T:                                                                                                \
-        e = (al && Geo<T>::bpb % 4 == 0) ? mg_launch_t<T, (Geo<T>::bpb % 4 == 0)>(a, mats[i].x, mats[i].ldx, \
-                                                                                 stream, e0, e1)           \
-                                         : mg_launch_t<T, false>(a, mats[i].x, mats[i].ldx, stream, e0, e1); \
+        e = (al && Geo<T>::bpb % 4 == 0)                                                                   \
+                ? mg_launch_tf<T, (Geo<T>::bpb % 4 == 0)>(a, tf, mats[i].x, mats[i].ldx, stream, e0, e1)  \
+                : mg_launch_tf<T, false>(a, tf, mats[i].x, mats[i].ldx, stream, e0, e1);                   \
         break;
         switch (type) {
             PYRITE_CASE(T_Q4_0) PYRITE_CASE(T_Q4_1) PYRITE_CASE(T_Q5_0) PYRITE_CASE(T_Q5_1)
