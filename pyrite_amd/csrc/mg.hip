@@ -191,10 +191,20 @@ __global__ __launch_bounds__(256) void mg_frag_kernel(const float* __restrict__ 
 // ---------------------------------------------------------------- GEMM
 typedef __attribute__((address_space(3))) void lds_void;
 
-// 64 lanes x 16 bytes from src (per lane) to dst .. dst + 1 KiB (wave-uniform)
+// 64 lanes x 16 bytes from src (per lane) to dst .. dst + 1 KiB (wave-uniform
+// LDS address, in M0).  Issued as inline assembly: the compiler then does not
+// treat every later LDS read as a possible reader of this copy (it would put
+// a wait for all outstanding loads before each, and so wait for the next
+// chunk's copies before computing this one).  Completion is waited for
+// explicitly (mg_wait_all) before the barrier that publishes the chunk.
 __device__ __forceinline__ void lds_load_1k(const uint4* src, uint4* dst) {
-    __builtin_amdgcn_global_load_lds(static_cast<const void*>(src), (lds_void*)(dst), 16, 0, 0);
+    const uint32_t m = __builtin_amdgcn_readfirstlane(
+        static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_void*)(dst))));
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
 }
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt unconstrained) as a builtin the
+// compiler's own wait placement sees: it then knows every earlier load is done
+__device__ __forceinline__ void mg_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 __device__ __forceinline__ h8v as_h8(const uint4 v) {
     const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -263,15 +273,17 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
     const uint4* xsrc = a.XF + (size_t)tt * TF * 64 + lane;
 
     // the chunk's fragments: fragment j = (fragment step j / TF, token fragment j % TF)
-    auto stage = [&](int ch, int buf) {
+    constexpr int KPW = (CF + kMgWaves - 1) / kMgWaves;  // copies per wave and chunk
+    auto stage_k = [&](int ch, int buf, int k) {
         const int x0 = ch * CX;
         const int nx = nxs - x0 < CX ? nxs - x0 : CX;
+        const int j = w + kMgWaves * k;
+        const int xl = j / TF, fl = j - xl * TF;
+        if (j < CF && xl < nx) lds_load_1k(xsrc + ((size_t)(x0 + xl) * a.Fp + fl) * 64, &abuf[buf][j * 64]);
+    };
+    auto stage = [&](int ch, int buf) {
 #pragma unroll
-        for (int k = 0; k < (CF + kMgWaves - 1) / kMgWaves; ++k) {
-            const int j = w + kMgWaves * k;
-            const int xl = j / TF, fl = j - xl * TF;
-            if (j < CF && xl < nx) lds_load_1k(xsrc + ((size_t)(x0 + xl) * a.Fp + fl) * 64, &abuf[buf][j * 64]);
-        }
+        for (int k = 0; k < KPW; ++k) stage_k(ch, buf, k);
     };
 
     // WL: this wave's row region; lane (row q / WP, piece q % WP) of copy k, q = 64 k + lane
@@ -311,7 +323,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
     for (int ch = 0; ch < nchunk; ++ch) {
         // this chunk's fragments have landed (all waves), and every wave is
         // done with the buffer the next chunk goes into
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        mg_wait_all();
         __syncthreads();
         if (ch + 1 < nchunk) stage(ch + 1, (ch + 1) & 1);
         const uint4* ab = abuf[ch & 1] + lane;
