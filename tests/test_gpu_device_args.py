@@ -78,9 +78,11 @@ def test_matvec_outputs_land_in_the_callers_tensor(q4k, dev, orc):
     x = torch.from_numpy(orc.normal(32, 2 * cols)).to(dev).reshape(2, cols)
     announce("device args", "in-place outputs")
     ref = device.matvec(12, w, x, rows, cols)
+    # batch 1 has a kernel of its own (another summation order than batch 2)
+    ref1 = device.matvec(12, w, x[:1], rows, cols)
     y1 = torch.zeros(rows, device=dev)
     device.matvec(12, w, x[0], rows, cols, out=y1)
-    assert torch.equal(y1, ref[0])
+    assert torch.equal(y1, ref1[0])
     padded = torch.zeros(2, rows + 8, device=dev)
     device.matvec(12, w, x, rows, cols, out=padded[:, :rows])
     assert torch.equal(padded[:, :rows], ref) and not padded[:, rows:].any()
