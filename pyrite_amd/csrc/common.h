@@ -253,6 +253,22 @@ __device__ __forceinline__ unsigned arrive_dev(unsigned* counter) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     return __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Arrival of workgroup k of n at a two-level counter tree: fan sub-counters
+// sub[0..fan) and a root; workgroup k arrives at sub[k % fan], the last of
+// each sub-counter's members at the root.  True for exactly one workgroup, the
+// last to arrive overall.  Leaves every sub-counter at zero; the root is left
+// at its final count, for the caller to reset.  Device-scope atomics on one
+// address are serialised (measured about 30 ns apart on MI355X), so n
+// arrivals on a single counter take n times that; the tree cuts the chain to
+// about n / fan + fan.  Same calling rules as arrive_dev.
+__device__ __forceinline__ bool arrive_tree(unsigned* sub, unsigned* root, unsigned fan, unsigned k, unsigned n) {
+    if (fan > n) fan = n;
+    const unsigned j = k % fan;
+    const unsigned members = (n - j + fan - 1) / fan;  // workgroups k' < n with k' % fan == j
+    if (arrive_dev(sub + j) != members - 1) return false;
+    st_dev(sub + j, 0u);
+    return arrive_dev(root) == fan - 1;
+}
 
 // ---------------------------------------------------------------- lane sums
 // GFX9 DPP controls: quad_perm [1,0,3,2] (lane ^ 1), quad_perm [2,3,0,1]

@@ -33,8 +33,10 @@
 namespace pyrite {
 
 constexpr int kLmWgs = 256;   // argmax workgroups per token
-constexpr int kLmCand = 32;   // candidates kept per workgroup before it reports overflow
+constexpr int kLmCand = 31;   // candidates kept per workgroup before it reports overflow
 constexpr int kLmKept = 512;  // candidates the deciding workgroup refines from LDS
+constexpr int kLmFan = 40;    // sub-counters of a token's arrival tree (arrive_tree)
+constexpr int kLmArr = 1 + kLmFan;  // arrival counters per token: the root, then the sub-counters
 
 struct LmArgs {
     int type;
@@ -55,7 +57,8 @@ struct LmArgs {
     int* ws_cnt;             // [batch][kLmWgs]  (-1: non-finite seen)
     int* ws_cand;            // [batch][kLmWgs][kLmCand]
     double* ws_candv;        // [batch][kLmWgs][kLmCand]: y + B of each listed row
-    unsigned int* ws_arrive; // [batch]
+    unsigned int* ws_arrive; // [batch][kLmArr]: root, sub-counters
+    unsigned int* ws_rec;    // fused batch-1 head: kLmRecDw dwords per workgroup (aliases the arrays above)
 };
 
 __device__ __forceinline__ double readlane_f64(double v, int k) {
@@ -91,27 +94,131 @@ __device__ __forceinline__ bool better(double v, int r, double bv, int br) {
     return v > bv || (v == bv && r < br);
 }
 
-__device__ __forceinline__ void block_best(double& bv, int& br, double* s_bv, int* s_br) {
+// LDS of a deciding workgroup.
+struct LmDecLds {
+    double red[4];
+    int flag[4];
+    int cnt, nref, one;  // candidate count, rows queued for recomputation, any candidate
+    int kept[kLmKept];
+    double bv[4];
+    int br[4];
+};
+
+__device__ __forceinline__ void block_best(double& bv, int& br, LmDecLds& sd) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     for (int off = 32; off > 0; off >>= 1) {
         const double ov = __shfl_xor(bv, off, 64);
         const int orr = __shfl_xor(br, off, 64);
         if (better(ov, orr, bv, br)) { bv = ov; br = orr; }
     }
-    if (lane == 0) { s_bv[wave] = bv; s_br[wave] = br; }
+    if (lane == 0) { sd.bv[wave] = bv; sd.br[wave] = br; }
     __syncthreads();
-    bv = s_bv[0];
-    br = s_br[0];
+    bv = sd.bv[0];
+    br = sd.br[0];
     for (int k = 1; k < 4; ++k)
-        if (better(s_bv[k], s_br[k], bv, br)) { bv = s_bv[k]; br = s_br[k]; }
+        if (better(sd.bv[k], sd.br[k], bv, br)) { bv = sd.bv[k]; br = sd.br[k]; }
+}
+
+// Block-wide max of a double and OR of a flag word (4 waves).
+__device__ __forceinline__ void block_max_or(double& v, int& f, LmDecLds& sd) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (int off = 32; off > 0; off >>= 1) {
+        v = fmax(v, __shfl_xor(v, off, 64));
+        f |= __shfl_xor(f, off, 64);
+    }
+    if (lane == 0) { sd.red[wave] = v; sd.flag[wave] = f; }
+    __syncthreads();
+    v = fmax(fmax(sd.red[0], sd.red[1]), fmax(sd.red[2], sd.red[3]));
+    f = sd.flag[0] | sd.flag[1] | sd.flag[2] | sd.flag[3];
+    __syncthreads();  // sd.red / sd.flag may be reused
+}
+
+// The decision for token t by one 256-thread workgroup, once every row's logit
+// and bound are stored and L (the largest lower bound y - B over all rows) is
+// known.  gather(consider) calls consider(row, y + B) for rows of this
+// thread's share that can reach L (a superset of the candidates is fine).
+// Leaves the token's arrival root at zero.  Logits and bounds are read
+// with device-scope loads: they may have been stored by other workgroups of
+// the same launch.
+template <class Gather>
+__device__ void lm_decide(const LmArgs& a, int t, double L, int any_nf, LmDecLds& sd, Gather gather) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float* y = a.Y + (unsigned long long)t * a.ldy;
+    const float* bn = a.Bnd + (unsigned long long)t * a.ldy;
+    const float* x = a.X + (unsigned long long)t * a.ldx;
+    unsigned* root = a.ws_arrive + (unsigned long long)t * kLmArr;
+    if (any_nf) {
+        // Full recomputation, then Python's max(): the first element is kept
+        // unless a later one compares strictly greater (NaN never does).
+        if (wave == 0) {
+            double best = 0.0;
+            int bi = 0;
+            for (int r = 0; r < a.rows; ++r) {
+                const double v = ref_row(a, r, x);
+                if (r == 0 || v > best) { best = v; bi = r; }
+            }
+            if (lane == 0) a.ids[t] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) st_dev(root, 0u);
+        return;
+    }
+
+    // Candidates: y + B >= L (less a relative slack for the rounding of the
+    // double sums); each is queued for recomputation.
+    const double Lc = L - fabs(L) * 0x1p-50;
+    if (tid == 0) { sd.cnt = 0; sd.nref = 0; sd.one = -1; }
+    __syncthreads();
+    auto consider = [&](int r, double h) {
+        if (h < Lc) return;
+        sd.one = r;  // any candidate; used only when there is exactly one
+        const int q = atomicAdd(&sd.nref, 1);
+        if (q < kLmKept) sd.kept[q] = r;
+    };
+    gather(consider);
+    __syncthreads();
+    const int nref = sd.nref;
+    if (nref == 1) {
+        if (tid == 0) { a.ids[t] = sd.one; st_dev(root, 0u); }
+        return;
+    }
+    // All-zero activations: every reference logit is +-0, which compare
+    // equal, so the first row wins.
+    int nz = 0;
+    for (int c = tid; c < a.cols; c += 256) nz |= (x[c] != 0.f);
+    double unused = 0.0;
+    block_max_or(unused, nz, sd);
+    if (!nz) {
+        if (tid == 0) { a.ids[t] = 0; st_dev(root, 0u); }
+        return;
+    }
+    double bv = -INFINITY;
+    int br = 0x7FFFFFFF;
+    for (int q = wave; q < (nref < kLmKept ? nref : kLmKept); q += 4) {
+        const int r = sd.kept[q];
+        const double v = ref_row(a, r, x);
+        if (better(v, r, bv, br)) { bv = v; br = r; }
+    }
+    if (nref > kLmKept) {
+        // more rows to recompute than fit the list: recompute every such row, one per wave
+        for (int r = wave; r < a.rows; r += 4) {
+            const double h = (double)ld_dev(y + r) + (a.gamma * (double)ld_dev(bn + r) + a.abs_margin);
+            if (h < Lc) continue;  // wave-uniform
+            const double v = ref_row(a, r, x);
+            if (better(v, r, bv, br)) { bv = v; br = r; }
+        }
+    }
+    block_best(bv, br, sd);
+    if (tid == 0) {
+        a.ids[t] = br == 0x7FFFFFFF ? -1 : br;
+        st_dev(root, 0u);
+    }
 }
 
 __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
     const int t = blockIdx.y, w = blockIdx.x, tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
     const float* y = a.Y + (unsigned long long)t * a.ldy;
     const float* bn = a.Bnd + (unsigned long long)t * a.ldy;
-    const float* x = a.X + (unsigned long long)t * a.ldx;
     const int chunk = (a.rows + kLmWgs - 1) / kLmWgs;
     const double g = a.gamma, am = a.abs_margin;
     auto range = [&](int k, int& q0, int& q1) {
@@ -121,12 +228,8 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
     auto hi = [&](int r) { return (double)y[r] + (g * (double)bn[r] + am); };
     auto lo = [&](int r) { return (double)y[r] - (g * (double)bn[r] + am); };
 
-    __shared__ double s_red[4];
-    __shared__ int s_flag[4];
-    __shared__ int s_cnt, s_nref, s_one, s_last;  // s_cnt: local candidate count (pass 2)
-    __shared__ int s_kept[kLmKept];
-    __shared__ double s_bv[4];
-    __shared__ int s_br[4];
+    __shared__ LmDecLds sd;
+    __shared__ int s_cnt, s_last;  // s_cnt: local candidate count (pass 2)
 
     int r0, r1;
     range(w, r0, r1);
@@ -138,15 +241,8 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
         if (!isfinite(y[r]) || !isfinite(l)) nf = 1;
         lmax = fmax(lmax, l);
     }
-    for (int off = 32; off > 0; off >>= 1) {
-        lmax = fmax(lmax, __shfl_xor(lmax, off, 64));
-        nf |= __shfl_xor(nf, off, 64);
-    }
-    if (lane == 0) { s_red[wave] = lmax; s_flag[wave] = nf; }
     if (tid == 0) s_cnt = 0;
-    __syncthreads();
-    lmax = fmax(fmax(s_red[0], s_red[1]), fmax(s_red[2], s_red[3]));
-    nf = s_flag[0] | s_flag[1] | s_flag[2] | s_flag[3];
+    block_max_or(lmax, nf, sd);
 
     // pass 2: rows that can still beat L_w (a superset of the token's candidates in this range)
     int* cand = a.ws_cand + ((unsigned long long)t * kLmWgs + w) * kLmCand;
@@ -168,8 +264,10 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
     }
     drain_dev();  // every wave's candidate stores have completed ...
     __syncthreads();
-    if (tid == 0) s_last = (arrive_dev(a.ws_arrive + t) == kLmWgs - 1);  // ... before the arrival
-    __syncthreads();
+    if (tid == 0) {  // ... before the arrival
+        unsigned* root = a.ws_arrive + (unsigned long long)t * kLmArr;
+        s_last = arrive_tree(root + 1, root, 16, w, kLmWgs);
+    }
     __syncthreads();
     if (!s_last) return;
 
@@ -178,88 +276,203 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
     const int my_cnt = ld_dev(a.ws_cnt + (unsigned long long)t * kLmWgs + tid);
     double L = ld_dev(a.ws_L + (unsigned long long)t * kLmWgs + tid);
     int any_nf = my_cnt < 0;
-    for (int off = 32; off > 0; off >>= 1) {
-        L = fmax(L, __shfl_xor(L, off, 64));
-        any_nf |= __shfl_xor(any_nf, off, 64);
-    }
-    if (lane == 0) { s_red[wave] = L; s_flag[wave] = any_nf; }
-    __syncthreads();
-    L = fmax(fmax(s_red[0], s_red[1]), fmax(s_red[2], s_red[3]));
-    any_nf = s_flag[0] | s_flag[1] | s_flag[2] | s_flag[3];
-
-    if (any_nf) {
-        // Full recomputation, then Python's max(): the first element is kept
-        // unless a later one compares strictly greater (NaN never does).
-        if (wave == 0) {
-            double best = 0.0;
-            int bi = 0;
-            for (int r = 0; r < a.rows; ++r) {
-                const double v = ref_row(a, r, x);
-                if (r == 0 || v > best) { best = v; bi = r; }
-            }
-            if (lane == 0) a.ids[t] = bi;
+    block_max_or(L, any_nf, sd);
+    lm_decide(a, t, L, any_nf, sd, [&](auto& consider) {
+        if (my_cnt > 0 && my_cnt <= kLmCand) {
+            const unsigned long long base = ((unsigned long long)t * kLmWgs + tid) * kLmCand;
+            for (int q = 0; q < my_cnt; ++q) consider(ld_dev(a.ws_cand + base + q), ld_dev(a.ws_candv + base + q));
+        } else if (my_cnt > kLmCand) {
+            int q0, q1;
+            range(tid, q0, q1);
+            for (int r = q0; r < q1; ++r) consider(r, hi(r));
         }
-        __syncthreads();
-        if (tid == 0) st_dev(a.ws_arrive + t, 0u);
-        return;
-    }
+    });
+}
 
-    // Candidates: y + B >= L (less a relative slack for the rounding of the
-    // double sums above); each is queued for recomputation.
+// ---------------------------------------------------------------- fused batch-1 head
+// For one vector the argmax rides on the bound matvec itself (lm_fused_kernel):
+// each slot's leader lane keeps, over the rows it finishes, the largest lower
+// bound y - B, and lists in the workgroup's LDS every row whose upper bound
+// y + B reaches it at that moment (a superset of the rows that can reach the
+// workgroup's final bound; a list that fills up marks the workgroup as
+// overflowed).  When its rows are done a workgroup publishes one record -- its
+// lower bound L_w and the listed rows that reach L_w -- and the last workgroup
+// to arrive decides with lm_decide.  An overflowed workgroup makes the decider
+// scan every row's stored logit and bound instead of the records.
+
+constexpr int kLmWgList = 128;       // rows a workgroup lists while it runs
+constexpr int kLmRecCand = 4;        // candidate rows a workgroup record holds
+// Record of a workgroup, 8 qwords: L_w, h0, (count, r0), (r1, r2), (r3, 0), h1, h2, h3 -- candidate
+// rows r and their y + B h, the largest h first (so a record whose h0 is below the deciding bound
+// holds no candidate).  Count -1: a non-finite value seen; kLmRecCand + 1: rows not listed.
+constexpr int kLmRecDw = 16;
+constexpr int kLmFusedWgsMax = 2048;
+constexpr int kLmRecPerThread = kLmFusedWgsMax / 256;  // records the decider's threads read each
+
+typedef __attribute__((address_space(3))) int lds_i;
+typedef __attribute__((address_space(3))) double lds_d;
+
+struct LmObs {
+    double g, am;
+    lds_i* n;     // rows listed (may exceed kLmWgList: overflow)
+    lds_i* lr;    // listed rows
+    lds_d* lh;    // their y + B
+    double lmax = -INFINITY;  // largest y - B this lane has seen
+    int nf = 0;               // a non-finite logit or lower bound seen
+
+    // Logits and bounds are stored with device-scope stores: the deciding
+    // workgroup of this launch may read them.
+    template <int B, int R>
+    __device__ __forceinline__ void row(const MvDesc& d, long long r, int ri, const float (&acc)[R][B],
+                                        const float (&bacc)[R][B], bool) {
+        static_assert(B == 1 && R == 1, "one vector, one row per slot");
+        const float y = acc[ri][0], s = bacc[ri][0];
+        st_dev(d.Y + r, y);
+        st_dev(d.Bnd + r, s);
+        const double bd = g * (double)s + am;
+        const double lo = (double)y - bd, hi = (double)y + bd;
+        if (!isfinite(y) || !isfinite(lo)) nf = 1;
+        lmax = fmax(lmax, lo);
+        if (hi >= lmax - fabs(lmax) * 0x1p-50) {
+            const int k = __hip_atomic_fetch_add(n, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+            if (k < kLmWgList) { lr[k] = (int)r; lh[k] = hi; }
+        }
+    }
+};
+
+template <int T, bool AL>
+__global__ __launch_bounds__(256) void lm_fused_kernel(const MvDesc d, const LmArgs a) {
+    // the staged activations are read 16 bytes at a time: their base (placed
+    // after the static LDS below) must be 16-byte aligned
+    extern __shared__ __attribute__((aligned(16))) float smem[];
+    __shared__ LmDecLds sd;
+    __shared__ int s_n;
+    __shared__ int s_lr[kLmWgList];
+    __shared__ double s_lh[kLmWgList];
+    __shared__ int s_cr[kLmRecCand];
+    __shared__ double s_cv[kLmRecCand];
+    __shared__ int s_last;
+    const int tid = threadIdx.x;
+
+    if (tid == 0) s_n = 0;
+    __syncthreads();
+    LmObs ob;
+    ob.g = a.gamma;
+    ob.am = a.abs_margin;
+    ob.n = (lds_i*)&s_n;
+    ob.lr = (lds_i*)s_lr;
+    ob.lh = (lds_d*)s_lh;
+    mv_body<T, 1, 1, AL, true, true, XDirect, 4, LmObs>(d, blockIdx.x, smem, ob);
+
+    // this workgroup's record
+    double lw = ob.lmax;
+    int fl = ob.nf;
+    if (tid == 0) sd.cnt = 0;
+    block_max_or(lw, fl, sd);  // its barrier also orders the list writes before the reads below
+    const int listed = s_n;
+    const bool nf = fl & 1, ovf = listed > kLmWgList;
+    if (!nf && !ovf && tid < listed) {
+        const double lc = lw - fabs(lw) * 0x1p-50;
+        if (s_lh[tid] >= lc) {
+            const int k = atomicAdd(&sd.cnt, 1);
+            if (k < kLmRecCand) { s_cr[k] = s_lr[tid]; s_cv[k] = s_lh[tid]; }
+        }
+    }
+    static_assert(kLmWgList <= 256, "one thread per listed row");
+    __syncthreads();
+    const int cnt = nf ? -1 : (ovf || sd.cnt > kLmRecCand) ? kLmRecCand + 1 : sd.cnt;
+    if (tid < kLmRecDw / 2) {
+        const int nc = cnt >= 0 && cnt <= kLmRecCand ? cnt : 0;  // candidates the record lists
+        int best = 0;
+        for (int k = 1; k < nc; ++k) best = s_cv[k] > s_cv[best] ? k : best;
+        auto row = [&](int k) {  // k-th listed row, the best first
+            const int kk = k == 0 ? best : k == best ? 0 : k;
+            return k < nc ? (unsigned long long)(unsigned)s_cr[kk] : 0ull;
+        };
+        auto hv = [&](int k) {
+            const int kk = k == 0 ? best : k == best ? 0 : k;
+            return k < nc ? (unsigned long long)__double_as_longlong(s_cv[kk]) : 0ull;
+        };
+        unsigned long long v = 0;
+        switch (tid) {
+        case 0: v = (unsigned long long)__double_as_longlong(lw); break;
+        case 1: v = hv(0); break;
+        case 2: v = (unsigned long long)(unsigned)cnt | (row(0) << 32); break;
+        case 3: v = row(1) | (row(2) << 32); break;
+        case 4: v = row(3); break;
+        default: v = hv(tid - 4); break;
+        }
+        st_dev(reinterpret_cast<unsigned long long*>(a.ws_rec) + (unsigned long long)blockIdx.x * (kLmRecDw / 2) + tid,
+               v);
+    }
+    drain_dev();  // every wave's logit, bound and record stores have completed ...
+    __syncthreads();
+    if (tid == 0) s_last = arrive_tree(a.ws_arrive + 1, a.ws_arrive, kLmFan, blockIdx.x, gridDim.x);  // ... before the arrival
+    __syncthreads();
+    if (!s_last) return;
+
+    // ---- deciding workgroup; thread t reads records t, t + 256, ..., all
+    // loads of a pass issued before any is used
+    const int nwg = (int)gridDim.x;
+    const unsigned long long* recs = reinterpret_cast<const unsigned long long*>(a.ws_rec);
+    unsigned long long q0[kLmRecPerThread], q1[kLmRecPerThread], q2[kLmRecPerThread];
+#pragma unroll
+    for (int i = 0; i < kLmRecPerThread; ++i) {
+        const int k = tid + 256 * i;
+        const unsigned long long* p = recs + (unsigned long long)(k < nwg ? k : 0) * (kLmRecDw / 2);
+        q0[i] = ld_dev(p);
+        q1[i] = ld_dev(p + 1);
+        q2[i] = ld_dev(p + 2);
+    }
+    double L = -INFINITY;
+    int f = 0;
+#pragma unroll
+    for (int i = 0; i < kLmRecPerThread; ++i) {
+        if (tid + 256 * i >= nwg) continue;
+        const int c = (int)(unsigned)q2[i];
+        L = fmax(L, __longlong_as_double((long long)q0[i]));
+        f |= (c < 0) | ((c > kLmRecCand) << 1);
+    }
+    block_max_or(L, f, sd);
+    const bool any_ovf = (f >> 1) & 1;
     const double Lc = L - fabs(L) * 0x1p-50;
-    if (tid == 0) { s_cnt = 0; s_nref = 0; s_one = -1; }
-    __syncthreads();
-    double bv = -INFINITY;
-    int br = 0x7FFFFFFF;
-    auto consider = [&](int r, double h) {
-        if (h < Lc) return;
-        s_one = r;  // any candidate; used only when there is exactly one
-        const int q = atomicAdd(&s_nref, 1);
-        if (q < kLmKept) s_kept[q] = r;
-    };
-    if (my_cnt > 0 && my_cnt <= kLmCand) {
-        const unsigned long long base = ((unsigned long long)t * kLmWgs + tid) * kLmCand;
-        for (int q = 0; q < my_cnt; ++q) consider(ld_dev(a.ws_cand + base + q), ld_dev(a.ws_candv + base + q));
-    } else if (my_cnt > kLmCand) {
-        int q0, q1;
-        range(tid, q0, q1);
-        for (int r = q0; r < q1; ++r) consider(r, hi(r));
-    }
-    __syncthreads();
-    const int nref = s_nref;
-    if (nref == 1) {
-        if (tid == 0) { a.ids[t] = s_one; st_dev(a.ws_arrive + t, 0u); }
-        return;
-    }
-    // All-zero activations: every reference logit is +-0, which compare
-    // equal, so the first row wins.
-    int nz = 0;
-    for (int c = tid; c < a.cols; c += 256) nz |= (x[c] != 0.f);
-    for (int off = 32; off > 0; off >>= 1) nz |= __shfl_xor(nz, off, 64);
-    if (lane == 0) s_flag[wave] = nz;
-    __syncthreads();
-    if (!(s_flag[0] | s_flag[1] | s_flag[2] | s_flag[3])) {
-        if (tid == 0) { a.ids[t] = 0; st_dev(a.ws_arrive + t, 0u); }
-        return;
-    }
-    for (int q = wave; q < (nref < kLmKept ? nref : kLmKept); q += 4) {
-        const int r = s_kept[q];
-        const double v = ref_row(a, r, x);
-        if (better(v, r, bv, br)) { bv = v; br = r; }
-    }
-    if (nref > kLmKept) {
-        // more rows to recompute than fit the list: recompute every such row, one per wave
-        for (int r = wave; r < a.rows; r += 4) {
-            if (hi(r) < Lc) continue;  // wave-uniform
-            const double v = ref_row(a, r, x);
-            if (better(v, r, bv, br)) { bv = v; br = r; }
+    lm_decide(a, 0, L, f & 1, sd, [&](auto& consider) {
+        if (any_ovf) {
+            // some workgroup did not list all its rows: every row's stored logit and bound, 8 rows a step
+            for (int r0 = 0; r0 < a.rows; r0 += 8 * 256) {
+                float yv[8], bv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    const int r = r0 + tid + 256 * u < a.rows ? r0 + tid + 256 * u : a.rows - 1;
+                    yv[u] = ld_dev(a.Y + r);
+                    bv[u] = ld_dev(a.Bnd + r);
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u)
+                    if (r0 + tid + 256 * u < a.rows)
+                        consider(r0 + tid + 256 * u, (double)yv[u] + (a.gamma * (double)bv[u] + a.abs_margin));
+            }
+            return;
         }
-    }
-    block_best(bv, br, s_bv, s_br);
-    if (tid == 0) {
-        a.ids[t] = br == 0x7FFFFFFF ? -1 : br;
-        st_dev(a.ws_arrive + t, 0u);
-    }
+#pragma unroll
+        for (int i = 0; i < kLmRecPerThread; ++i) {
+            const int k = tid + 256 * i;
+            const double h0 = __longlong_as_double((long long)q1[i]);
+            const int c = (int)(unsigned)q2[i];
+            if (k >= nwg || c < 1 || !(h0 >= Lc)) continue;  // h0 is the record's largest
+            consider((int)(q2[i] >> 32), h0);
+            if (c > 1) {
+                const unsigned long long* p = recs + (unsigned long long)k * (kLmRecDw / 2);
+                const unsigned long long r12 = ld_dev(p + 3), r3 = ld_dev(p + 4);
+                const double h1 = __longlong_as_double((long long)ld_dev(p + 5));
+                const double h2 = __longlong_as_double((long long)ld_dev(p + 6));
+                const double h3 = __longlong_as_double((long long)ld_dev(p + 7));
+                consider((int)(unsigned)r12, h1);
+                if (c > 2) consider((int)(r12 >> 32), h2);
+                if (c > 3) consider((int)(unsigned)r3, h3);
+            }
+        }
+    });
 }
 
 // ---------------------------------------------------------------- workspace
@@ -267,13 +480,15 @@ __global__ __launch_bounds__(256) void lm_argmax_kernel(const LmArgs a) {
 struct LmWorkspace {
     void* bnd = nullptr;     // float [tokens][ldl]
     size_t bnd_cap = 0;      // bytes
-    void* tok = nullptr;     // per token: L, cnt, cand, candv (kLmTokBytes), then arrival counters
+    void* tok = nullptr;     // per token: L, cnt, cand, candv (kLmTokBytes); then kLmArr arrival counters per token
     size_t tok_cap = 0;      // bytes
 };
 
 // Per-token workspace bytes: L (double) and cnt (int) per argmax workgroup,
 // then its candidate rows (int) and their upper bounds (double).
 constexpr size_t kLmTokBytes = (size_t)kLmWgs * (8 + 4 + kLmCand * (4 + 8));
+// ... and with its arrival counters
+constexpr size_t kLmTokTotal = kLmTokBytes + kLmArr * sizeof(unsigned int);
 
 // Carve the token arrays out of one block of `tokens` tokens (arrival counters last).
 static void lm_carve(void* base, size_t tokens, LmArgs& a) {
@@ -300,7 +515,7 @@ static int lm_workspace(size_t bnd_floats, size_t tokens, hipStream_t stream, Lm
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return -4;
     LmWorkspace& w = ws[dev];
-    const size_t bb = bnd_floats * sizeof(float), tb = tokens * (kLmTokBytes + sizeof(unsigned int));
+    const size_t bb = bnd_floats * sizeof(float), tb = tokens * kLmTokTotal;
     hipError_t e = hipSuccess;
     if (bb > w.bnd_cap) e = workspace_grow(&w.bnd, &w.bnd_cap, bb, false, stream);
     if (e == hipSuccess && tb > w.tok_cap) {
@@ -340,25 +555,96 @@ static double lm_gamma(const TypeGeo& g, size_t cols) {
     return (g32 + g64) * (1 + 1.0 / 1024);
 }
 
-// Zero the arrival counters of `n` tokens (a kernel, not a memset, so that it
-// can be captured into a graph).
+// Zero n arrival counters (a kernel, not a memset, so that it can be
+// captured into a graph).
 __global__ __launch_bounds__(256) void lm_clear_kernel(unsigned int* counters, int n) {
     for (int i = threadIdx.x; i < n; i += 256) counters[i] = 0u;
 }
 
-// The bound matvec, then the argmax kernel, over workspace memory the caller
-// provides: bnd (floats laid out like the logits) and a token block carved by
-// lm_carve for `tok_cap` tokens.  clear: zero the arrival counters first.
+// PYRITE_LM_FUSED=0 keeps batch-1 heads on the two-kernel path (bound matvec,
+// then lm_argmax_kernel).
+static bool lm_fused_env() {
+    static const bool on = [] {
+        const char* e = getenv("PYRITE_LM_FUSED");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+// Workgroups resident per CU of one fused kernel instance.
+template <int T, bool AL>
+static int lm_fused_per_cu(size_t lds) {
+    static const int n = [lds] {
+        int v = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, lm_fused_kernel<T, AL>, 256, lds) != hipSuccess || v < 1)
+            v = 1;
+        return v;
+    }();
+    return n;
+}
+
+// Launch the fused head for one vector; 1 when the matrix is not eligible
+// (plain types, activations that do not fit LDS, unaligned weights of a
+// dword-multiple block format), which then takes the two-kernel path.
+template <int T>
+static int lm_fused_launch_t(bool al, const MatvecArgs& m, float* bnd, const LmArgs& a, size_t max_recs,
+                             hipStream_t stream) {
+    if constexpr (Geo<T>::bs == 1) {
+        return 1;
+    } else {
+        constexpr bool AL = Geo<T>::bpb % 4 == 0;
+        if ((AL && !al) || !use_xl<T, 1, true>((int)m.cols)) return 1;
+        const size_t lds = lds_bytes<T, 1, true>((int)m.cols, true);
+        if (lds + 4096 > 65536) return 1;  // the kernel's own LDS (under 4 KiB) comes on top
+        MvDesc d{};
+        d.W = static_cast<const uint8_t*>(m.w);
+        d.row_bytes = m.cols / Geo<T>::bs * Geo<T>::bpb;
+        d.X = m.x;
+        d.ldx = m.ldx;
+        d.Y = m.y;
+        d.ldy = m.ldy;
+        d.rows = (int)m.rows;
+        d.cols = (int)m.cols;
+        d.lpr_log2 = mat_shape<T, 1, AL>(d.rows, d.cols).lpr_log2;
+        d.Bnd = bnd;
+        const long long rows_per_wg = (long long)kMvWaves * (64 >> d.lpr_log2);
+        long long nwg = (long long)lm_fused_per_cu<T, AL>(lds) * dev_info().cus;
+        const long long need = ((long long)m.rows + rows_per_wg - 1) / rows_per_wg;
+        if (need < nwg) nwg = need;
+        if (nwg > kLmFusedWgsMax) nwg = kLmFusedWgsMax;
+        if ((size_t)nwg > max_recs) nwg = (long long)max_recs;
+        if (nwg < 1) return -4;
+        d.wg_begin = 0;
+        d.wg_count = (int)nwg;
+        hipLaunchKernelGGL((lm_fused_kernel<T, AL>), dim3((unsigned)nwg), dim3(256), lds, stream, d, a);
+        return hipGetLastError() == hipSuccess ? 0 : -4;
+    }
+}
+
+static int lm_fused_launch(int type, bool al, const MatvecArgs& m, float* bnd, const LmArgs& a, size_t max_recs,
+                           hipStream_t stream) {
+#define PYRITE_CASE(T) \
+    case T: return lm_fused_launch_t<T>(al, m, bnd, a, max_recs, stream);
+    switch (type) {
+        PYRITE_FOR_EACH_TYPE(PYRITE_CASE)
+    default: return 1;
+    }
+#undef PYRITE_CASE
+}
+
+// Tokens' worth of workspace the fused head's records need (its workgroup
+// records alias the per-token arrays).
+constexpr size_t kLmFusedTokens = (kLmFusedWgsMax * kLmRecDw * 4 + kLmTokBytes - 1) / kLmTokBytes;
+
+// The bound matvec, then the argmax kernel (or, for one vector, the fused
+// kernel that does both), over workspace memory the caller provides: bnd
+// (floats laid out like the logits) and a token block carved by lm_carve for
+// `tok_cap` tokens.  clear: zero the arrival counters first.
 static int lm_head_run(int type, const TypeGeo& g, bool al, size_t max_cols, const MatvecArgs& m, int* ids,
                        size_t batch, float* bnd, void* tok, size_t tok_cap, bool clear, hipStream_t stream) {
     LmArgs a;
     lm_carve(tok, tok_cap, a);
-    if (clear) {
-        hipLaunchKernelGGL(lm_clear_kernel, dim3(1), dim3(256), 0, stream, a.ws_arrive, (int)batch);
-        if (hipGetLastError() != hipSuccess) return -4;
-    }
-    if (const int rc = valu_group_launch<true>(type, g, al, &m, &bnd, 1, batch, max_cols, stream, nullptr, nullptr))
-        return rc;
+    a.ws_rec = static_cast<unsigned int*>(tok);
     a.type = type;
     a.bs = g.bs;
     a.bpb = g.bpb;
@@ -374,6 +660,16 @@ static int lm_head_run(int type, const TypeGeo& g, bool al, size_t max_cols, con
     a.gamma = lm_gamma(g, m.cols);
     a.abs_margin = 1e-30;
     a.ids = ids;
+    if (clear) {
+        hipLaunchKernelGGL(lm_clear_kernel, dim3(1), dim3(256), 0, stream, a.ws_arrive, (int)(batch * kLmArr));
+        if (hipGetLastError() != hipSuccess) return -4;
+    }
+    if (batch == 1 && lm_fused_env()) {
+        const int rc = lm_fused_launch(type, al, m, bnd, a, tok_cap * kLmTokBytes / (kLmRecDw * 4), stream);
+        if (rc != 1) return rc;
+    }
+    if (const int rc = valu_group_launch<true>(type, g, al, &m, &bnd, 1, batch, max_cols, stream, nullptr, nullptr))
+        return rc;
     hipLaunchKernelGGL(lm_argmax_kernel, dim3(kLmWgs, (unsigned)batch), dim3(256), 0, stream, a);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
@@ -400,24 +696,26 @@ int lm_head_launch(int type, const uint8_t* W, size_t w_len, size_t rows, size_t
                                    &max_cols))
         return rc;
     LmWorkspace* ws = nullptr;
-    if (const int rc = lm_workspace(batch * ldl, batch, stream, &ws)) return rc;
+    if (const int rc = lm_workspace(batch * ldl, batch > kLmFusedTokens ? batch : kLmFusedTokens, stream, &ws))
+        return rc;
     return lm_head_run(type, g, al, max_cols, m, ids, batch, static_cast<float*>(ws->bnd), ws->tok,
-                       ws->tok_cap / (kLmTokBytes + sizeof(unsigned int)), false, stream);
+                       ws->tok_cap / kLmTokTotal, false, stream);
 }
 
 // ---------------------------------------------------------------- allocation-free variant
 // The LM head for callers that cannot allocate (code under graph capture,
 // serving loops): its workspace is this file-scope device array instead of
 // hipMalloc'ed memory.  Layout: the token block for kLmScratchTokens tokens
-// (lm_carve), then, from the next 256-byte boundary, the bound floats.  Each
+// (lm_carve), then, from byte kLmScratchBndOffset, the bound floats.  Each
 // GPU holds its own copy until the process ends; every call on a GPU shares it
 // (the last call's contents stay), so calls that overlap on one GPU race.
 constexpr size_t kLmScratchBytes = size_t(8) << 20;
 constexpr size_t kLmScratchTokens = 8;
-constexpr size_t kLmScratchBndOffset =
-    (kLmScratchTokens * (kLmTokBytes + sizeof(unsigned int)) + 255) & ~size_t(255);
+constexpr size_t kLmScratchBndOffset = 811264;
+static_assert(kLmScratchTokens * kLmTokTotal <= kLmScratchBndOffset, "the token block ends before the bounds");
 constexpr size_t kLmScratchBndFloats = (kLmScratchBytes - kLmScratchBndOffset) / sizeof(float);
 static_assert(kLmScratchBndFloats == 1894336, "the limit quoted in the error message and the header");
+static_assert(kLmScratchTokens >= kLmFusedTokens, "the fused head's records fit the scratch token block");
 
 static __device__ __align__(256) unsigned char scratch[kLmScratchBytes];
 

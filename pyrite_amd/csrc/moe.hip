@@ -629,7 +629,8 @@ __global__ __launch_bounds__(kMvThreads) void moe_mv_kernel(const MoeMvArgs a) {
         d.pad = 0;
         d.Bnd = nullptr;
         __syncthreads();  // the previous item's waves are done with LDS
-        mv_body<T, MB, 1, AL, XL, false, XS>(d, 0, smem);
+        NoObs ob;
+        mv_body<T, MB, 1, AL, XL, false, XS>(d, 0, smem, ob);
     }
 }
 

@@ -123,12 +123,28 @@ __device__ __forceinline__ void consume(const Raw (&raw)[R]) {
     }
 }
 
+// What a slot's leader lane does with each finished row: NoObs stores the
+// logits (and bounds) to d.Y / d.Bnd; another observer (the fused LM head)
+// may store them its own way and watch the values go by.  Called for rows
+// below d.rows only.
+struct NoObs {
+    template <int B, int R>
+    __device__ __forceinline__ void row(const MvDesc& d, long long r, int ri, const float (&acc)[R][B],
+                                        const float (&bacc)[R][B], bool bd) {
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            d.Y[b * d.ldy + r] = acc[ri][b];
+            if (bd) d.Bnd[b * d.ldy + r] = bacc[ri][b];
+        }
+    }
+};
+
 // XL: activations staged in LDS (padded, see XView) instead of read from
 // global memory by every unit; used when B * cols fits the LDS budget.
 // BD: also accumulate each row's magnitude sum (Unit::bound, or sum |w||x| for
 // plain types) and store it to d.Bnd.
-template <int T, int B, int R, bool AL, bool XL, bool BD, class XS = XDirect, int NW = kMvWaves>
-__device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* smem) {
+template <int T, int B, int R, bool AL, bool XL, bool BD, class XS = XDirect, int NW = kMvWaves, class OB = NoObs>
+__device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* smem, OB& ob) {
     static_assert(XL || std::is_same<XS, XDirect>::value, "indirect activations need LDS staging");
     constexpr int BS = Geo<T>::bs, BPB = Geo<T>::bpb;
     const uint8_t* __restrict__ W = d.W;
@@ -161,12 +177,7 @@ __device__ __forceinline__ void mv_body(const MvDesc& d, long long wg, float* sm
         if (li == 0) {
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (r0 + r < rows)
-#pragma unroll
-                    for (int b = 0; b < B; ++b) {
-                        d.Y[b * d.ldy + r0 + r] = acc[r][b];
-                        if constexpr (BD) d.Bnd[b * d.ldy + r0 + r] = bacc[r][b];
-                    }
+                if (r0 + r < rows) ob.template row<B, R>(d, r0 + r, r, acc, bacc, BD);
         }
 #pragma unroll
         for (int r = 0; r < R; ++r)
@@ -348,7 +359,8 @@ __global__ __launch_bounds__(64 * NW) void mv_kernel(const MvGroup g) {
     extern __shared__ float smem[];
     int i = 0;
     while (i + 1 < g.n && (int)blockIdx.x >= g.d[i + 1].wg_begin) ++i;
-    mv_body<T, B, R, AL, XL, BD, XS, NW>(g.d[i], (long long)blockIdx.x - g.d[i].wg_begin, smem);
+    NoObs ob;
+    mv_body<T, B, R, AL, XL, BD, XS, NW>(g.d[i], (long long)blockIdx.x - g.d[i].wg_begin, smem, ob);
 }
 
 // ---------------------------------------------------------------- launcher

@@ -72,6 +72,16 @@ def test_lm_head_random_types(orc, dev, t):
     _check(orc, dev, t, payload, rows, cols, xs, "random")
 
 
+@pytest.mark.parametrize("t", [14, 8, 12, 13, 2, 23, 11, 10, 3, 7, 20])
+def test_lm_head_random_types_one_vector(orc, dev, t):
+    """One vector: the argmax is decided inside the bound matvec (its own kernel)."""
+    rng = np.random.default_rng(200 + t)
+    rows, cols = 5000, 1024
+    payload = _random_q(rng, t, rows, cols)
+    x = orc.normal(7100 + t, cols)
+    _check(orc, dev, t, payload, rows, cols, x[None, :], "random one vector")
+
+
 @pytest.mark.parametrize("t", [0, 1, 30, 24])
 def test_lm_head_plain_types(orc, dev, t):
     """Float and integer heads from seeded N(0, 0.02) weights (x 100 for I8)."""
@@ -156,6 +166,8 @@ def test_lm_head_zero_activations(orc, dev):
     xs = np.zeros((2, cols), dtype=np.float32)
     ids = _check(orc, dev, t, payload, rows, cols, xs, "zero-x")
     assert list(ids) == [0, 0]
+    ids = _check(orc, dev, t, payload, rows, cols, xs[:1], "zero-x one vector")
+    assert list(ids) == [0]
 
 
 def test_lm_head_nonfinite_activation(orc, dev):
