@@ -2,31 +2,38 @@
 //   Y[t][r] = sum_c dequant(W)[r][c] * X[t][c]   for t < batch
 // (pyrite/kernels/native.c:518-555 applied to every token; fp32 accumulation).
 //
-// Operands and exact fp16 fragments are those of mx_traits.h: A = activations
-// (MFMA row m = 2t + p, fp16 hi (p = 0) and lo (p = 1) parts of x[t]), B =
-// weights built exactly from the block codes, D = per lane row r0 + n of W and
-// token-parts 4g..4g+3.  The block scales are applied once per block.
+// Operands of v_mfma_f32_16x16x32_f16 (lane l: m or n = l % 16, K-slot group
+// g = l / 16): A = activations of 16 tokens (row m = token), one fragment for
+// the fp16 "hi" parts of x * 2^-e_t and one for the "lo" parts; B = weights
+// built exactly from the block codes (mx_traits.h); D = per lane weight row
+// r0 + n and tokens 4g..4g+3.  The hi and the lo fragment are multiplied by
+// the same B into the same accumulator, so a block's D holds one value per
+// (token, row) and the block scales are applied once per block.
 //
 // Three launches:
-//   mg_exp_kernel   one wave per token: the power of two e_t that brings the
-//                   token's largest finite |x| into [2^14, 2^15);
-//   mg_frag_kernel  x[t] * 2^-e_t as fp16 hi/lo A fragments, written in the
-//                   order the GEMM reads them: XF[(xs * Fp + f) * 64 + lane]
-//                   is lane `lane`'s 16 bytes of fragment step xs for tokens
-//                   8f..8f+7 (1 KiB per fragment).  Fragment steps are the
-//                   32-column steps, and for formats with per-sub-block mins
-//                   (MINSUM) one more per block: the tokens' sums over each
-//                   32-column sub-block, times 2^-e_t-5, in K-slots 0..7;
+//   mg_exp_kernel   one workgroup per token: the power of two e_t that brings
+//                   the token's largest finite |x| into [2^14, 2^15);
+//   mg_frag_kernel  x[t] * 2^-e_t as fp16 hi and lo A fragments, written in
+//                   the order the GEMM reads them: XF[((xs * Gp + f) * 2 + p)
+//                   * 64 + lane] is lane `lane`'s 16 bytes of part p (0 hi,
+//                   1 lo) of fragment step xs for tokens 16f..16f+15 (1 KiB
+//                   per fragment).  Fragment steps are the 32-column steps,
+//                   and for formats with per-sub-block mins (MINSUM) one
+//                   more per block: the tokens' sums over each 32-column
+//                   sub-block times 2^-e_t-5, hi parts in K-slots 0..7 and lo
+//                   parts in K-slots 8..15 of part 0;
 //   mg_kernel       the GEMM.  A workgroup of 8 waves owns 256 rows of one
-//                   matrix (32 per wave = two 16-row MFMA tiles) and 8 * TF
+//                   matrix (32 per wave = two 16-row MFMA tiles) and 16 * TG
 //                   tokens.  K is walked in chunks of 8 steps: the chunk's
 //                   fragments go from XF into LDS by direct global -> LDS
-//                   loads (no registers), one chunk ahead, and each wave
-//                   builds each weight block's B fragments once (codes loaded
-//                   one block ahead into registers) and multiplies them
-//                   against all TF token fragments.  MINSUM formats take
-//                   their min term as one MFMA per block against the staged
-//                   sums.  The result is scaled by 2^e_t once, at the end.
+//                   loads (no registers), one chunk ahead.  Each wave builds
+//                   each weight block's B fragments once (codes loaded one
+//                   block ahead into registers), reads the next step's A
+//                   fragments from LDS while it multiplies the current ones,
+//                   and multiplies every B against all TG token groups.
+//                   MINSUM formats take their min term as one MFMA per block
+//                   against the staged sums.  The result is scaled by 2^e_t
+//                   once, at the end.
 // Two waves per SIMD (at most 256 registers each) let one wave's fragment
 // building run under the other's MFMAs.  Workgroups are mapped so that all
 // token tiles of one row tile run on one XCD, next to each other: their
@@ -55,12 +62,11 @@ template <class F> struct MgMinSum<F, std::void_t<decltype(F::MINSUM)>> : std::b
 template <class F>
 constexpr int mg_xs_per_block() { return F::STEPS + (MgMinSum<F>::value ? 1 : 0); }
 
-// 8-token fragments per workgroup: up to 8 for MINSUM formats (one
-// accumulator per block), 4 for the others (two), so that a wave fits in 256
-// registers.  Launches whose 32-token workgroups fit in one pass over the
-// CUs take 4.
+// 16-token groups per workgroup: up to 4 for MINSUM formats (one accumulator
+// per block), 2 for the others (two), so that a wave fits in 256 registers.
+// Launches whose 32-token workgroups fit in one pass over the CUs take 2.
 template <class F>
-constexpr int mg_tf_max() { return MgMinSum<F>::value ? 8 : 4; }
+constexpr int mg_tg_max() { return MgMinSum<F>::value ? 4 : 2; }
 
 struct MgMat {
     const uint8_t* W;
@@ -76,7 +82,7 @@ struct MgArgs {
     int nmat;
     const uint4* XF;
     const int* texp;
-    int Fp;  // fragments per fragment step in XF (token tiles * TF)
+    int Gp;  // 16-token groups per fragment step in XF (token tiles * TG)
     int cols, batch;
     int row_tiles, tok_tiles;
 };
@@ -111,56 +117,54 @@ __global__ __launch_bounds__(256) void mg_exp_kernel(const float* __restrict__ X
     if (tid == 0) texp[t] = norm_exp(fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3])));
 }
 
-// Workgroup (token fragment f, 256-column window sb): the 8 tokens' window
-// is read row by row into LDS, then thread (step s, K-slot group g, token
-// 8f + tp) writes the hi and lo 16 bytes of its 8 columns.  MINSUM formats
-// (256-column blocks, K-slot map 1) also write the block's sums step: lane
-// group 0, rows 2 tp + p hold the hi / lo parts of the token's eight
-// sub-block sums (times 2^-e_t-5), the other lanes zeros.
+// Workgroup (16-token group f, 256-column window sb): the 16 tokens' window
+// is read row by row into LDS, then item (step s, K-slot group g, token m)
+// writes the hi and lo 16 bytes of its 8 columns as lane 16 g + m of parts 0
+// and 1 (two items per thread).  MINSUM formats (256-column blocks, K-slot
+// map 1) also write the block's sums step: in part 0, lane group 0 holds the
+// hi and lane group 1 the lo parts of the token's eight sub-block sums (times
+// 2^-e_t-5), the other lanes and part 1 zeros.
 template <int T>
 __global__ __launch_bounds__(256) void mg_frag_kernel(const float* __restrict__ X, unsigned long long ldx, int cols,
                                                       int batch, const int* __restrict__ texp, uint4* __restrict__ XF,
-                                                      int Fp) {
+                                                      int Gp) {
     using F = Mx<T>;
     constexpr bool MS = MgMinSum<F>::value;
     constexpr int KM = MxKMode<F>::value;
     constexpr int XPB = mg_xs_per_block<F>();
     constexpr int LD = 256 + 4;  // LDS row pitch (floats)
     static_assert(!MS || (F::STEPS == 8 && KM == 1), "sums step: 256-column blocks, K-slot map 1");
-    __shared__ float xs[8 * LD];
-    __shared__ float sums[MS ? 64 : 1];
+    __shared__ float xs[16 * LD];
+    __shared__ float sums[MS ? 128 : 1];
     const int tid = threadIdx.x, nsteps = cols / 32, sg = (nsteps + 7) / 8;
     const int f = blockIdx.x / sg, sb = blockIdx.x - f * sg;
-    {
-        const int tr = tid >> 5, c = 256 * sb + 8 * (tid & 31);
-        float4 u = make_float4(0.f, 0.f, 0.f, 0.f), w = u;
-        if (8 * f + tr < batch && c < cols) {
-            const float* q = X + (unsigned long long)(8 * f + tr) * ldx + c;
-            u = ld_x4(q);
-            w = ld_x4(q + 4);
-        }
-        float* d = xs + tr * LD + 8 * (tid & 31);
-        *reinterpret_cast<float4*>(d) = u;
-        *reinterpret_cast<float4*>(d + 4) = w;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int q = tid + 256 * k, tr = q >> 6, c = 256 * sb + 4 * (q & 63);
+        float4 u = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (16 * f + tr < batch && c < cols) u = ld_x4(X + (unsigned long long)(16 * f + tr) * ldx + c);
+        *reinterpret_cast<float4*>(xs + tr * LD + 4 * (q & 63)) = u;
     }
     __syncthreads();
-    const int sl = tid >> 5, tp = tid & 7, g = (tid >> 3) & 3;
-    const int t = 8 * f + tp;
-    const int e = t < batch ? texp[t] : 0;
-    if (8 * sb + sl < nsteps) {
-        const int off = KM == 1 ? 64 * g + 8 * sl : 32 * sl + 8 * g;
-        const float4 u = *reinterpret_cast<const float4*>(xs + tp * LD + off);
-        const float4 w = *reinterpret_cast<const float4*>(xs + tp * LD + off + 4);
-        const float v[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
-        uint4 hi, lo;
-        split8(v, e, hi, lo);
-        const int xstep = MS ? sb * XPB + sl : 8 * sb + sl;
-        uint4* o = XF + ((size_t)xstep * Fp + f) * 64 + g * 16 + 2 * tp;
-        o[0] = hi;
-        o[1] = lo;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int it = tid + 256 * h, sl = it >> 6, g = (it >> 4) & 3, m = it & 15;
+        const int t = 16 * f + m;
+        if (8 * sb + sl < nsteps) {
+            const int off = KM == 1 ? 64 * g + 8 * sl : 32 * sl + 8 * g;
+            const float4 u = *reinterpret_cast<const float4*>(xs + m * LD + off);
+            const float4 w = *reinterpret_cast<const float4*>(xs + m * LD + off + 4);
+            const float v[8] = {u.x, u.y, u.z, u.w, w.x, w.y, w.z, w.w};
+            uint4 hi, lo;
+            split8(v, t < batch ? texp[t] : 0, hi, lo);
+            const int xstep = MS ? sb * XPB + sl : 8 * sb + sl;
+            uint4* o = XF + ((size_t)xstep * Gp + f) * 128 + 16 * g + m;
+            o[0] = hi;
+            o[64] = lo;
+        }
     }
     if constexpr (MS) {
-        if (tid < 64) {
+        if (tid < 128) {
             // sub-block j = tid & 7 of token tid >> 3: columns 32 j .. 32 j + 31
             const float* q = xs + (tid >> 3) * LD + 32 * (tid & 7);
             float acc = 0.f;
@@ -172,18 +176,19 @@ __global__ __launch_bounds__(256) void mg_frag_kernel(const float* __restrict__ 
             sums[tid] = acc;
         }
         __syncthreads();
-        if (tid < 64) {
+        if (tid < 128) {
+            const int p = tid >> 6, ln = tid & 63, g = ln >> 4, m = ln & 15;
             uint4 r = make_uint4(0u, 0u, 0u, 0u);
-            if (tid < 16) {
-                const int tq = tid >> 1, tk = 8 * f + tq;
+            if (p == 0 && g < 2) {
+                const int tk = 16 * f + m;
                 float sv[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) sv[j] = sums[tq * 8 + j];
+                for (int j = 0; j < 8; ++j) sv[j] = sums[m * 8 + j];
                 uint4 hi, lo;
                 split8(sv, (tk < batch ? texp[tk] : 0) + 5, hi, lo);
-                r = (tid & 1) ? lo : hi;
+                r = g ? lo : hi;
             }
-            XF[((size_t)(sb * XPB + 8) * Fp + f) * 64 + tid] = r;
+            XF[((size_t)(sb * XPB + 8) * Gp + f) * 128 + tid] = r;
         }
     }
 }
@@ -211,7 +216,7 @@ __device__ __forceinline__ h8v as_h8(const uint4 v) {
     return __builtin_bit_cast(h8v, w);
 }
 
-template <int T, bool AL, int TF>
+template <int T, bool AL, int TG>
 __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
     using F = Mx<T>;
     constexpr bool MS = MgMinSum<F>::value;
@@ -219,8 +224,9 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
     constexpr int NA = MS ? 1 : F::NACC;                                 // accumulators per block
     constexpr int BPC = F::STEPS >= kMgChunk ? 1 : kMgChunk / F::STEPS;  // blocks per chunk
     constexpr int XPB = mg_xs_per_block<F>();
-    constexpr int CX = BPC * XPB;  // fragment steps per chunk
-    constexpr int CF = CX * TF;    // fragments per chunk
+    constexpr int CX = BPC * XPB;    // fragment steps per chunk
+    constexpr int FS = 2 * TG;       // fragments per fragment step (groups x hi/lo)
+    constexpr int CF = CX * FS;      // fragments per chunk
     // Super-block formats other than MINSUM ones (unaligned 84- to 210-byte
     // blocks): each wave copies its 32 rows' next block into its own LDS
     // region with aligned 16-byte direct loads (the 16-byte pieces that
@@ -270,16 +276,17 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
     const int nblk = a.cols / F::BS;
     const int nchunk = (nblk + BPC - 1) / BPC;
     const int nxs = nblk * XPB;
-    const uint4* xsrc = a.XF + (size_t)tt * TF * 64 + lane;
+    // this workgroup's groups are contiguous in each fragment step
+    const uint4* xsrc = a.XF + (size_t)tt * FS * 64 + lane;
 
-    // the chunk's fragments: fragment j = (fragment step j / TF, token fragment j % TF)
+    // the chunk's fragments: fragment j = (fragment step j / FS, group and part j % FS)
     constexpr int KPW = (CF + kMgWaves - 1) / kMgWaves;  // copies per wave and chunk
     auto stage_k = [&](int ch, int buf, int k) {
         const int x0 = ch * CX;
         const int nx = nxs - x0 < CX ? nxs - x0 : CX;
         const int j = w + kMgWaves * k;
-        const int xl = j / TF, fl = j - xl * TF;
-        if (j < CF && xl < nx) lds_load_1k(xsrc + ((size_t)(x0 + xl) * a.Fp + fl) * 64, &abuf[buf][j * 64]);
+        const int xl = j / FS, fl = j - xl * FS;
+        if (j < CF && xl < nx) lds_load_1k(xsrc + ((size_t)(x0 + xl) * a.Gp * 2 + fl) * 64, &abuf[buf][j * 64]);
     };
     auto stage = [&](int ch, int buf) {
 #pragma unroll
@@ -314,9 +321,9 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
     }
     stage(0, 0);
 
-    f4v acc[TF][NT];
+    f4v acc[TG][NT];
 #pragma unroll
-    for (int f = 0; f < TF; ++f)
+    for (int f = 0; f < TG; ++f)
 #pragma unroll
         for (int i = 0; i < NT; ++i) acc[f][i] = f4v{0.f, 0.f, 0.f, 0.f};
 
@@ -348,34 +355,50 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
             typename MxPreOf<F>::type pre[NT];
 #pragma unroll
             for (int i = 0; i < NT; ++i) mx_prep<F>(ca[i], g, pre[i]);
-            const uint4* fb = ab + (b - b0) * XPB * TF * 64;
-            f4v D[TF][NT][NA];
+            // fragment (step st, group f, part p) of this block at fb[(st * FS + 2 f + p) * 64]
+            const uint4* fb = ab + (b - b0) * XPB * FS * 64;
+            f4v D[TG][NT][NA];
+            // A fragments of the current step, and of the next one in flight
+            uint4 Av[2][FS];
+#pragma unroll
+            for (int q = 0; q < FS; ++q) Av[0][q] = fb[q * 64];
 #pragma unroll
             for (int st = 0; st < F::STEPS; ++st) {
+                const int cur = st & 1;
+                if (st + 1 < F::STEPS) {
+#pragma unroll
+                    for (int q = 0; q < FS; ++q) Av[cur ^ 1][q] = fb[((st + 1) * FS + q) * 64];
+                } else if constexpr (MS) {
+                    // the sums step: part 0 of each group
+#pragma unroll
+                    for (int f = 0; f < TG; ++f) Av[cur ^ 1][2 * f] = fb[(F::STEPS * FS + 2 * f) * 64];
+                }
                 uint32_t B[NT][NA][4];
 #pragma unroll
                 for (int i = 0; i < NT; ++i) {
                     if constexpr (MS) F::frag_main(ca[i], pre[i], st, B[i][0]);
                     else mx_frag<F>(ca[i], pre[i], st, g, B[i]);
                 }
-                // all of the step's token fragments requested at once
-                uint4 Av[TF];
+                // hi parts of every group first, then the lo parts: the two
+                // products into one accumulator are never back to back
 #pragma unroll
-                for (int f = 0; f < TF; ++f) Av[f] = fb[(st * TF + f) * 64];
+                for (int pt = 0; pt < 2; ++pt)
 #pragma unroll
-                for (int f = 0; f < TF; ++f) {
-                    const h8v A = as_h8(Av[f]);
+                    for (int f = 0; f < TG; ++f) {
+                        const h8v A = as_h8(Av[cur][2 * f + pt]);
 #pragma unroll
-                    for (int i = 0; i < NT; ++i)
+                        for (int i = 0; i < NT; ++i)
 #pragma unroll
-                        for (int p = 0; p < NA; ++p)
-                            D[f][i][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-                                A, __builtin_bit_cast(h8v, B[i][p]),
-                                st == 0 ? f4v{0.f, 0.f, 0.f, 0.f} : D[f][i][p], 0, 0, 0);
-                }
+                            for (int p = 0; p < NA; ++p)
+                                D[f][i][p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                                    A, __builtin_bit_cast(h8v, B[i][p]),
+                                    (st == 0 && pt == 0) ? f4v{0.f, 0.f, 0.f, 0.f} : D[f][i][p], 0, 0, 0);
+                    }
             }
             if constexpr (MS) {
-                // acc += d D - dmin (sum_j 32 m_j * 2^-5 S_j)
+                // acc += d D - dmin (sum_j 32 m_j * 2^-5 S_j), the sums' hi and
+                // lo parts in K-slots 0..7 and 8..15 against 32 m_j in both
+                constexpr int cm = F::STEPS & 1;  // Av buffer holding the sums
                 float dm[NT];
                 uint32_t Bm[NT][4];
 #pragma unroll
@@ -384,22 +407,22 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
                     dm[i] = -F::mscale(ca[i]);
                     F::min_frag(ca[i], g, Bm[i]);
 #pragma unroll
-                    for (int f = 0; f < TF; ++f) {
+                    for (int f = 0; f < TG; ++f) {
                         f4v& q = acc[f][i];
 #pragma unroll
                         for (int k = 0; k < 4; ++k) q[k] = fmaf(d, D[f][i][0][k], q[k]);
                     }
                 }
 #pragma unroll
-                for (int f = 0; f < TF; ++f) {
-                    const h8v A = as_h8(fb[(F::STEPS * TF + f) * 64]);
+                for (int f = 0; f < TG; ++f) {
+                    const h8v A = as_h8(Av[cm][2 * f]);
 #pragma unroll
                     for (int i = 0; i < NT; ++i)
                         D[f][i][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                             A, __builtin_bit_cast(h8v, Bm[i]), f4v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
                 }
 #pragma unroll
-                for (int f = 0; f < TF; ++f)
+                for (int f = 0; f < TG; ++f)
 #pragma unroll
                     for (int i = 0; i < NT; ++i) {
                         f4v& q = acc[f][i];
@@ -408,7 +431,7 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
                     }
             } else {
 #pragma unroll
-                for (int f = 0; f < TF; ++f)
+                for (int f = 0; f < TG; ++f)
 #pragma unroll
                     for (int i = 0; i < NT; ++i) F::epi(ca[i], D[f][i], acc[f][i]);
             }
@@ -419,19 +442,21 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
         }
     }
 
-    // D rows 4g..4g+3 = (token 2g: hi, lo), (token 2g + 1: hi, lo) of each fragment
+    // D rows 4g..4g+3 = tokens 4g..4g+3 of each group
 #pragma unroll
-    for (int f = 0; f < TF; ++f) {
-        const int t0 = (tt * TF + f) * 8 + 2 * g;
-        const int e0 = t0 < a.batch ? a.texp[t0] : 0, e1 = t0 + 1 < a.batch ? a.texp[t0 + 1] : 0;
+    for (int f = 0; f < TG; ++f) {
+        const int t0 = (tt * TG + f) * 16 + 4 * g;
+        int ex[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ex[k] = t0 + k < a.batch ? a.texp[t0 + k] : 0;
 #pragma unroll
         for (int i = 0; i < NT; ++i) {
             const long long row = rbase + 16 * i;
             if (row >= rows) continue;
             const f4v v = acc[f][i];
-            if (t0 < a.batch) Y[(unsigned long long)t0 * ldy + row] = __builtin_amdgcn_ldexpf(v[0] + v[1], e0);
-            if (t0 + 1 < a.batch)
-                Y[(unsigned long long)(t0 + 1) * ldy + row] = __builtin_amdgcn_ldexpf(v[2] + v[3], e1);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (t0 + k < a.batch) Y[(unsigned long long)(t0 + k) * ldy + row] = __builtin_amdgcn_ldexpf(v[k], ex[k]);
         }
     }
 }
@@ -446,12 +471,12 @@ struct MgWorkspace {
 };
 static MgWorkspace g_mg_ws[64];
 
-template <int T, bool AL, int TF>
+template <int T, bool AL, int TG>
 static hipError_t mg_launch_t(MgArgs& a, const float* X, unsigned long long ldx, hipStream_t s, hipEvent_t e0,
                               hipEvent_t e1) {
     using F = Mx<T>;
     const int nsteps = a.cols / 32, nblk = a.cols / F::BS;
-    const size_t frag_bytes = (size_t)nblk * mg_xs_per_block<F>() * a.Fp * 1024;
+    const size_t frag_bytes = (size_t)nblk * mg_xs_per_block<F>() * a.Gp * 2048;
     const size_t need = frag_bytes + ((size_t)a.batch * sizeof(int) + 255) / 256 * 256;
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -463,36 +488,36 @@ static hipError_t mg_launch_t(MgArgs& a, const float* X, unsigned long long ldx,
     int* texp = reinterpret_cast<int*>(static_cast<uint8_t*>(ws.block) + frag_bytes);
     a.XF = XF;
     a.texp = texp;
-    const dim3 gexp(a.batch), gfrag((unsigned)((long long)a.Fp * ((nsteps + 7) / 8)));
+    const dim3 gexp(a.batch), gfrag((unsigned)((long long)a.Gp * ((nsteps + 7) / 8)));
     if (e0)
         hipExtLaunchKernelGGL(mg_exp_kernel, gexp, dim3(256), 0, s, e0, nullptr, 0, X, ldx, a.cols, texp);
     else
         hipLaunchKernelGGL(mg_exp_kernel, gexp, dim3(256), 0, s, X, ldx, a.cols, texp);
     hipLaunchKernelGGL((mg_frag_kernel<T>), gfrag, dim3(256), 0, s, X, ldx, a.cols, a.batch, (const int*)texp, XF,
-                       a.Fp);
+                       a.Gp);
     const unsigned wgs = (unsigned)((long long)a.row_tiles * a.tok_tiles);
     if (e1)
-        hipExtLaunchKernelGGL((mg_kernel<T, AL, TF>), dim3(wgs), dim3(kMgWaves * 64), 0, s, nullptr, e1, 0, a);
+        hipExtLaunchKernelGGL((mg_kernel<T, AL, TG>), dim3(wgs), dim3(kMgWaves * 64), 0, s, nullptr, e1, 0, a);
     else
-        hipLaunchKernelGGL((mg_kernel<T, AL, TF>), dim3(wgs), dim3(kMgWaves * 64), 0, s, a);
+        hipLaunchKernelGGL((mg_kernel<T, AL, TG>), dim3(wgs), dim3(kMgWaves * 64), 0, s, a);
     return hipGetLastError();
 }
 
-// fragments per workgroup for a launch of `row_tiles` row tiles
+// 16-token groups per workgroup for a launch of `row_tiles` row tiles
 template <int T>
-static int mg_tf_for(long long row_tiles, size_t batch) {
-    constexpr int TM = mg_tf_max<Mx<T>>();
+static int mg_tg_for(long long row_tiles, size_t batch) {
+    constexpr int TM = mg_tg_max<Mx<T>>();
     // 32-token tiles when they still fit in one pass over the 256 CUs
-    if (TM == 8 && row_tiles * (long long)((batch + 31) / 32) <= 256) return 4;
+    if (TM == 4 && row_tiles * (long long)((batch + 31) / 32) <= 256) return 2;
     return TM;
 }
 
 template <int T, bool AL>
-static hipError_t mg_launch_tf(MgArgs& a, int tf, const float* X, unsigned long long ldx, hipStream_t s,
+static hipError_t mg_launch_tg(MgArgs& a, int tg, const float* X, unsigned long long ldx, hipStream_t s,
                                hipEvent_t e0, hipEvent_t e1) {
-    if constexpr (mg_tf_max<Mx<T>>() == 8)
-        if (tf == 8) return mg_launch_t<T, AL, 8>(a, X, ldx, s, e0, e1);
-    return mg_launch_t<T, AL, 4>(a, X, ldx, s, e0, e1);
+    if constexpr (mg_tg_max<Mx<T>>() == 4)
+        if (tg == 4) return mg_launch_t<T, AL, 4>(a, X, ldx, s, e0, e1);
+    return mg_launch_t<T, AL, 2>(a, X, ldx, s, e0, e1);
 }
 
 // One launch set per run of consecutive matrices with the same activations
@@ -520,8 +545,8 @@ int mg_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, bo
             d.tile0 = (int)tiles;
             tiles += (long long)((mats[k].rows + kMgRows - 1) / kMgRows);
         }
-        int tf = 0;
-#define PYRITE_CASE(T) case T: tf = mg_tf_for<T>(tiles, batch); break;
+        int tg = 0;
+#define PYRITE_CASE(T) case T: tg = mg_tg_for<T>(tiles, batch); break;
         switch (type) {
             PYRITE_CASE(T_Q4_0) PYRITE_CASE(T_Q4_1) PYRITE_CASE(T_Q5_0) PYRITE_CASE(T_Q5_1)
             PYRITE_CASE(T_Q8_0) PYRITE_CASE(T_Q8_1) PYRITE_CASE(T_Q2_K) PYRITE_CASE(T_Q3_K)
@@ -533,17 +558,17 @@ int mg_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, bo
         a.cols = (int)mats[i].cols;
         a.batch = (int)batch;
         a.row_tiles = (int)tiles;
-        a.tok_tiles = (int)((batch + 8 * tf - 1) / (8 * tf));
-        a.Fp = a.tok_tiles * tf;
-        if (tiles * a.tok_tiles > 0x7FFFFFFFLL || (long long)a.Fp * ((a.cols / 32 + 7) / 8) > 0x7FFFFFFFLL)
+        a.tok_tiles = (int)((batch + 16 * tg - 1) / (16 * tg));
+        a.Gp = a.tok_tiles * tg;
+        if (tiles * a.tok_tiles > 0x7FFFFFFFLL || (long long)a.Gp * ((a.cols / 32 + 7) / 8) > 0x7FFFFFFFLL)
             return -2;
         hipEvent_t e0 = i == 0 ? start : nullptr, e1 = j == n ? stop : nullptr;
         hipError_t e = hipSuccess;
 #define PYRITE_CASE(T)                                                                                     \
     case T:                                                                                                \
         e = (al && Geo<T>::bpb % 4 == 0)                                                                   \
-                ? mg_launch_tf<T, (Geo<T>::bpb % 4 == 0)>(a, tf, mats[i].x, mats[i].ldx, stream, e0, e1)  \
-                : mg_launch_tf<T, false>(a, tf, mats[i].x, mats[i].ldx, stream, e0, e1);                   \
+                ? mg_launch_tg<T, (Geo<T>::bpb % 4 == 0)>(a, tg, mats[i].x, mats[i].ldx, stream, e0, e1)  \
+                : mg_launch_tg<T, false>(a, tg, mats[i].x, mats[i].ldx, stream, e0, e1);                   \
         break;
         switch (type) {
             PYRITE_CASE(T_Q4_0) PYRITE_CASE(T_Q4_1) PYRITE_CASE(T_Q5_0) PYRITE_CASE(T_Q5_1)

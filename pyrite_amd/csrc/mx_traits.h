@@ -321,12 +321,13 @@ template <> struct Mx<T_Q4_K> {
         b[2] = pk_fma(bias_lo(x1), p.S[h], p.O[h]);
         b[3] = pk_fma(bias_hi(x1), p.S[h], p.O[h]);
     }
-    // B of the min MFMA: K-slot j < 8 (lane group 0) holds 32 m_j (exact:
+    // B of the min MFMA: K-slots j and 8 + j (lane groups 0 and 1, against
+    // the hi and lo parts of the staged sub-block sums) hold 32 m_j (exact:
     // at most 2016), the other K-slots 0.  The staged sums carry 2^-5.
     __device__ __forceinline__ static void min_frag(const Raw& r, int g, uint32_t (&b)[4]) {
         const uint32_t m03 = r.hd[2] & 0x3F3F3F3Fu;
         const uint32_t m47 = ((r.hd[3] >> 4) & 0x0F0F0F0Fu) | ((r.hd[2] >> 2) & 0x30303030u);
-        const float sc = g == 0 ? 32.f : 0.f;
+        const float sc = g < 2 ? 32.f : 0.f;
         const uint32_t S = splat_h(sc), O = splat_h(-1024.f * sc);
         b[0] = pk_fma(bias_lo(m03), S, O);
         b[1] = pk_fma(bias_hi(m03), S, O);
