@@ -53,11 +53,28 @@ __device__ __forceinline__ void moe_router_row(int type, const uint8_t* __restri
     if (type == T_F32 && (H & 3) == 0 && ((reinterpret_cast<uintptr_t>(rp) | reinterpret_cast<uintptr_t>(x)) & 15) == 0) {
         const float4* w4 = reinterpret_cast<const float4*>(rp);
         const float4* x4 = reinterpret_cast<const float4*>(x);
-        for (int c = lane; c < H / 4; c += 64) {
-            const float4 w = w4[c], v = x4[c];
-            const double p0 = (double)w.x * v.x, p1 = (double)w.y * v.y, p2 = (double)w.z * v.z, p3 = (double)w.w * v.w;
-            acc += (p0 + p1) + (p2 + p3);
-            mag += (fabs(p0) + fabs(p1)) + (fabs(p2) + fabs(p3));
+        const int n4 = H / 4;
+        // eight float4 pairs per lane requested before any is used (one
+        // memory round trip for a 2048-column row instead of eight); the sum
+        // order per lane stays column-ascending
+        for (int c0 = lane; c0 < n4; c0 += 64 * 8) {
+            float4 w[8], v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                // past the row: the last float4 again (not used below)
+                const int c = c0 + 64 * k < n4 ? c0 + 64 * k : n4 - 1;
+                w[k] = w4[c];
+                v[k] = x4[c];
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                // no branch here: the loads above stay ahead of every use
+                const bool in = c0 + 64 * k < n4;
+                const double p0 = (double)w[k].x * v[k].x, p1 = (double)w[k].y * v[k].y;
+                const double p2 = (double)w[k].z * v[k].z, p3 = (double)w[k].w * v[k].w;
+                acc += in ? (p0 + p1) + (p2 + p3) : 0.0;
+                mag += in ? (fabs(p0) + fabs(p1)) + (fabs(p2) + fabs(p3)) : 0.0;
+            }
         }
     } else {
         for (int c = lane; c < H; c += 64) {
