@@ -231,6 +231,24 @@ __device__ __forceinline__ uint32_t spread4(uint32_t v) {
 // counter only after its own stores have completed (s_waitcnt 0).  The reader
 // runs only after observing the final count.  Nothing spins: a workgroup that
 // is not last simply exits.
+//
+// Why this is enough (an argument about gfx950 hardware, not the C++ memory
+// model, under which relaxed atomics alone would not order the stores before
+// the reads):
+//   1. an agent-scope atomic store or load is performed at the device-coherent
+//      level (it does not stay in or read from one XCD's L2), so every
+//      agent-scope access to an address sees one order of values;
+//   2. s_waitcnt 0 returns only after the wave's earlier stores have been
+//      acknowledged by that level, so they precede the counter increment,
+//      which is itself performed there;
+//   3. the deciding workgroup issues its loads only after the increment's
+//      returned value (the final count) has arrived and been branched on, and
+//      a wave issues memory instructions in program order, so each load is
+//      performed after every contributor's stores.
+// Callers: the split-K sum of the MFMA matvec (mx.hip), the LM-head argmax
+// and fused head (lmhead.hip), the MoE router/routing hand-offs and plan
+// (moe.hip).  The library builds for gfx950 only; another target would need
+// this argument checked again.
 template <typename V>
 __device__ __forceinline__ void st_dev(V* p, V v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
