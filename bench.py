@@ -25,7 +25,9 @@ peak), and the GGUF -> HBM upload rate of the resident-tensor loader.
 
 cpu_baseline: the reference's own native.c (oracle/_ref, built from the
 reference source) timed on the host on a bounded sample of the headline
-workload (whole decode layers, 7 single-vector pyrite_matvec calls each).
+workload (whole decode layers, 7 single-vector pyrite_matvec calls each) by
+the C harness oracle/cpu_bench.c: one warm-up pass, median of 5 timed runs,
+on one thread and on all host cores (at most 16).
 
 Prints one JSON line.  --gpus N > 1 exits: this path runs on one GPU.
 """
@@ -115,9 +117,15 @@ def llama_weights(np, quantize):
     return out
 
 
-def run_cpu_baseline(calls, budget_s: float, what: str):
-    """Time the reference's scalar fp64 pyrite_matvec on one host core over
-    `calls` [(type, payload, x, rows, cols)], repeated until budget_s passes."""
+def run_cpu_baseline(np, calls, budget_s: float, nthreads: int, what: str, runs: int = 5):
+    """Time the reference's scalar fp64 pyrite_matvec (oracle/_ref; the oracle's
+    restatement when that build is absent) over `calls` [(type, payload, x, rows,
+    cols)] with the C harness oracle/cpu_bench.c: one warm-up pass, then `runs`
+    timed runs of P passes each (P sized so the runs take about budget_s), the
+    median run reported; no Python in the timed region.  With nthreads > 1,
+    thread i runs every call on its own i-th share of each matrix's rows."""
+    import ctypes
+
     from oracle.oracle import oracle, reference
 
     impl = reference()
@@ -125,71 +133,41 @@ def run_cpu_baseline(calls, budget_s: float, what: str):
     if impl is None:
         impl = oracle()
         kind = "port"
-    done_bytes = 0
-    passes = 0
-    t0 = time.perf_counter()
-    while True:
-        for t, payload, x, rows, cols in calls:
-            impl.matvec(t, payload, x, rows, cols)
-            done_bytes += payload.nbytes
-        passes += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": done_bytes / dt / 1e9, "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": f"{passes} pass(es) of {what} through pyrite_matvec, single thread, {dt:.1f} s"}
+    h = ctypes.CDLL(str(ROOT / "oracle" / "libcpubench.so"))
+    sz, vp = ctypes.c_size_t, ctypes.c_void_p
+    h.cpu_bench_run.restype = ctypes.c_int
+    h.cpu_bench_run.argtypes = [vp, ctypes.c_int, vp, vp, vp, vp, vp, vp, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                vp]
+    n = len(calls)
+    payloads = [np.ascontiguousarray(p, dtype=np.uint8) for _, p, _, _, _ in calls]
+    xs = [np.ascontiguousarray(x, dtype=np.float64) for _, _, x, _, _ in calls]
+    types = np.array([t for t, *_ in calls], dtype=np.int32)
+    rows = np.array([r for *_, r, _ in calls], dtype=np.uint64)
+    cols = np.array([c for *_, c in calls], dtype=np.uint64)
+    rbytes = np.array([p.nbytes // r for p, r in zip(payloads, rows)], dtype=np.uint64)
+    wptr = np.array([p.ctypes.data for p in payloads], dtype=np.uint64)
+    xptr = np.array([x.ctypes.data for x in xs], dtype=np.uint64)
+    fn = ctypes.cast(impl._mv, vp).value
 
+    def timed(nruns, passes):
+        out = np.zeros(nruns, dtype=np.float64)
+        rc = h.cpu_bench_run(fn, n, types.ctypes.data, wptr.ctypes.data, rows.ctypes.data, cols.ctypes.data,
+                             rbytes.ctypes.data, xptr.ctypes.data, nthreads, nruns, passes, out.ctypes.data)
+        if rc != 0:
+            raise RuntimeError(f"cpu_bench_run failed: {rc}")
+        return out
 
-def run_cpu_baseline_parallel(calls, budget_s: float, nthreads: int, what: str):
-    """The same calls on several host cores: thread i runs every call on its own
-    contiguous i-th share of each matrix's rows (the reference function is
-    reentrant and rows are independent), so the threads never wait for each
-    other; throughput = all threads' bytes over the wall time."""
-    import threading
-
-    import numpy as np
-
-    from oracle.oracle import oracle, reference
-
-    impl = reference() or oracle()
-    done = [0] * nthreads
-    passes = [0] * nthreads
-    errors = []
-    start = threading.Barrier(nthreads + 1)
-    deadline = [0.0]
-
-    def worker(i):
-        outs = {}
-        start.wait()
-        while True:
-            for t, payload, x, rows, cols in calls:
-                rb = payload.nbytes // rows
-                r0, r1 = rows * i // nthreads, rows * (i + 1) // nthreads
-                if r1 <= r0:
-                    continue
-                out = outs.setdefault((rows, r1 - r0), np.zeros(r1 - r0, dtype=np.float64))
-                if impl.matvec_raw(t, payload[r0 * rb:r1 * rb], x, out, r1 - r0, cols) != 0:
-                    errors.append(t)
-                    return
-                done[i] += (r1 - r0) * rb
-            passes[i] += 1
-            if time.perf_counter() >= deadline[0]:
-                return
-
-    threads = [threading.Thread(target=worker, args=(i,)) for i in range(nthreads)]
-    for th in threads:
-        th.start()
-    t0 = time.perf_counter()
-    deadline[0] = t0 + budget_s
-    start.wait()
-    for th in threads:
-        th.join()
-    dt = time.perf_counter() - t0
-    if errors:
-        raise ValueError("pyrite_matvec failed")
-    return {"value": sum(done) / dt / 1e9, "unit": "GB/s", "cores": nthreads,
-            "sample": f"{min(passes)}-{max(passes)} pass(es) of {what} per thread, thread i on its i-th share "
-                      f"of every matrix's rows, {nthreads} threads, {dt:.1f} s"}
+    one = float(timed(1, 1)[0])  # calibration: one pass
+    passes = max(1, int(round(budget_s / runs / max(one, 1e-6))))
+    run_s = timed(runs, passes)
+    med = float(np.median(run_s))
+    bytes_per_pass = sum(p.nbytes for p in payloads)
+    return {"value": bytes_per_pass * passes / med / 1e9, "unit": "GB/s", "cores": nthreads, "kind": kind,
+            "sample": f"median of {runs} timed runs of {passes} pass(es) of {what} through pyrite_matvec "
+                      f"(runs {run_s.min():.2f}-{run_s.max():.2f} s, one warm-up pass), "
+                      + ("single thread" if nthreads == 1 else
+                         f"{nthreads} threads, thread i on its i-th share of every matrix's rows")
+                      + ", C harness oracle/cpu_bench.c"}
 
 
 def timed_grouped(lib, stream, sptr, launches, steps):
@@ -729,12 +707,13 @@ def main() -> int:
         calls = [(t, p, xv[cols], rows, cols) for t, rows, cols, p in mats.values()]
         what = "the Llama-3-8B layer decode (q, k, v, o, gate, up, down; one vector)"
         log(f"cpu baseline (~{args.cpu_seconds:.0f} s)")
-        cpu = run_cpu_baseline(calls, args.cpu_seconds, what)
+        cpu = run_cpu_baseline(np, calls, args.cpu_seconds, 1, what)
         model, ncpu = cpu_info()
         cpu["host"] = f"{model}, {ncpu} logical CPUs visible"
         nthreads = max(1, min(16, ncpu))  # all host cores (at most 16, the box's CPU share)
         log(f"cpu baseline on {nthreads} threads (~{args.cpu_seconds:.0f} s)")
-        cpu["all_cores"] = run_cpu_baseline_parallel(calls, args.cpu_seconds, nthreads, what)
+        cpu["all_cores"] = run_cpu_baseline(np, calls, args.cpu_seconds, nthreads, what)
+        del cpu["all_cores"]["kind"]
 
     moe = (extra or {}).get("moe_qwen3_30b_a3b") or {}
     result = {
