@@ -11,7 +11,8 @@
 // the contiguous byte slice e * rows * row_bytes (pyrite/qwen3_moe.py:364-398).
 //
 // Kernels, all on one stream, no host round trip:
-//   moe_router_kernel   fp64 router logits (tree order) and sum |w x| per row
+//   moe_router_kernel   fp64 router logits (tree order) and sum |w x| per row,
+//                       one expert row against four tokens per wave
 //   moe_router_route_kernel  router and routing in one launch for up to 16
 //                       tokens (the last of a token's workgroups routes it)
 //   moe_route_kernel    per token: exact ranking (rows whose rounding
@@ -90,18 +91,78 @@ __device__ __forceinline__ void moe_router_row(int type, const uint8_t* __restri
     }
 }
 
-// One wave per (expert row, token).
-__global__ __launch_bounds__(64) void moe_router_kernel(int type, const uint8_t* __restrict__ W,
-                                                        unsigned long long row_bytes, int E, int H, int bs, int bpb,
-                                                        const float* __restrict__ X, unsigned long long ldx,
-                                                        double* __restrict__ logits, double* __restrict__ mags) {
-    const int b = blockIdx.y;
-    const int e = blockIdx.x;
-    double acc, mag;
-    moe_router_row(type, W + (unsigned long long)e * row_bytes, H, bs, bpb, X + (unsigned long long)b * ldx, acc, mag);
-    if (threadIdx.x == 0) {
-        logits[(unsigned long long)b * E + e] = acc;
-        mags[(unsigned long long)b * E + e] = mag;
+constexpr int kMoeRouterTok = 4;  // tokens per wave of moe_router_kernel
+
+// Workgroup (x, y): wave w computes expert row 4x + w against tokens
+// 4y .. 4y + 3, each (row, token) logit and magnitude sum formed exactly as
+// moe_router_row forms it.  F32 rows (the Qwen3 case) are read once for the
+// four tokens: a batch of a lane's eight float4s of the row and of each
+// token's activations is requested before any is used.
+__global__ __launch_bounds__(256) void moe_router_kernel(int type, const uint8_t* __restrict__ W,
+                                                         unsigned long long row_bytes, int E, int H, int bs, int bpb,
+                                                         const float* __restrict__ X, unsigned long long ldx,
+                                                         int batch, double* __restrict__ logits,
+                                                         double* __restrict__ mags) {
+    constexpr int NT = kMoeRouterTok;
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int t0 = blockIdx.y * NT;
+    if (e >= E) return;  // wave-uniform; no barrier below
+    const uint8_t* rp = W + (unsigned long long)e * row_bytes;
+    const float* x0 = X + (unsigned long long)t0 * ldx;
+    double acc[NT], mag[NT];
+    const bool f32 = type == T_F32 && (H & 3) == 0 && (ldx & 3) == 0 &&
+                     ((reinterpret_cast<uintptr_t>(rp) | reinterpret_cast<uintptr_t>(x0)) & 15) == 0;
+    if (f32) {
+        const float4* w4 = reinterpret_cast<const float4*>(rp);
+        const int n4 = H / 4;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = mag[t] = 0.0;
+        for (int c0 = lane; c0 < n4; c0 += 64 * 8) {
+            float4 w[8], v[NT][8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                // past the row: the last float4 again (not used below)
+                const int c = c0 + 64 * k < n4 ? c0 + 64 * k : n4 - 1;
+                w[k] = w4[c];
+#pragma unroll
+                for (int t = 0; t < NT; ++t) {
+                    // tokens past the batch read the last token (not stored)
+                    const int tt = t0 + t < batch ? t0 + t : batch - 1;
+                    v[t][k] = reinterpret_cast<const float4*>(X + (unsigned long long)tt * ldx)[c];
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) {
+                    const bool in = c0 + 64 * k < n4;
+                    const double p0 = (double)w[k].x * v[t][k].x, p1 = (double)w[k].y * v[t][k].y;
+                    const double p2 = (double)w[k].z * v[t][k].z, p3 = (double)w[k].w * v[t][k].w;
+                    acc[t] += in ? (p0 + p1) + (p2 + p3) : 0.0;
+                    mag[t] += in ? (fabs(p0) + fabs(p1)) + (fabs(p2) + fabs(p3)) : 0.0;
+                }
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            for (int off = 32; off > 0; off >>= 1) {
+                acc[t] += __shfl_xor(acc[t], off, 64);
+                mag[t] += __shfl_xor(mag[t], off, 64);
+            }
+    } else {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const int tt = t0 + t < batch ? t0 + t : batch - 1;
+            moe_router_row(type, rp, H, bs, bpb, X + (unsigned long long)tt * ldx, acc[t], mag[t]);
+        }
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            if (t0 + t >= batch) break;
+            logits[(unsigned long long)(t0 + t) * E + e] = acc[t];
+            mags[(unsigned long long)(t0 + t) * E + e] = mag[t];
+        }
     }
 }
 
@@ -822,47 +883,68 @@ __global__ __launch_bounds__(256) void moe_xfrag_kernel(const float* X, unsigned
                                                         uint4* xf, int* xe,
                                                         unsigned* amax) {
     __shared__ unsigned tok_max[kMoeMxTok];
+    __shared__ int tok_id[kMoeMxTok];
     const int chunk = blockIdx.x;
     if (chunk >= totals[1]) return;
     const int pair0 = chunk * kMoeMxTok;
     const int tid = threadIdx.x;
     if (tid < kMoeMxTok) {
         tok_max[tid] = 0u;
+        tok_id[tid] = pair_tok[pair0 + tid];
         amax[pair0 + tid] = 0u;
     }
     __syncthreads();
+    // item idx = (step st, K-slot group gg, token t): 8 columns of token t;
+    // each thread takes items tid + 256 j, 8 at a time, every load of a batch
+    // issued before any is used
+    constexpr int kB = 8;
     const int steps = cols >> 5, count = steps * 4 * kMoeMxTok;
-    auto load8 = [&](int idx, int& t, int& gg, int& st, float (&v)[8]) {
-        t = idx % kMoeMxTok;
-        gg = (idx / kMoeMxTok) & 3;
-        st = idx / (4 * kMoeMxTok);
-        const int tok = pair_tok[pair0 + t];
-        if (tok < 0) {
+    auto load_batch = [&](int base, float (&v)[kB][8]) {
+        float4 q[kB][2];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) v[i] = 0.f;
-            return;
+        for (int j = 0; j < kB; ++j) {
+            const int idx = base + tid + 256 * j;
+            const int t = idx % kMoeMxTok, gg = (idx / kMoeMxTok) & 3, st = idx / (4 * kMoeMxTok);
+            const int tok = idx < count ? tok_id[t] : -1;
+            // padding pairs and items past the end read token 0's first columns (not used)
+            const float* p = X + (tok < 0 ? 0ull : (unsigned long long)tok * ldx + mx_kcol(kmode, st, gg));
+            q[j][0] = ld_x4(p);
+            q[j][1] = ld_x4(p + 4);
         }
-        const float* p = X + (unsigned long long)tok * ldx + mx_kcol(kmode, st, gg);
-        const float4 x0 = ld_x4(p), x1 = ld_x4(p + 4);
-        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w; v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+            const int idx = base + tid + 256 * j;
+            const bool use = idx < count && tok_id[idx % kMoeMxTok] >= 0;
+            const float4 x0 = q[j][0], x1 = q[j][1];
+            const float w[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[j][i] = use ? w[i] : 0.f;
+        }
     };
-    for (int idx = tid; idx < count; idx += 256) {
-        int t, gg, st;
-        float v[8];
-        load8(idx, t, gg, st, v);
-        const float mx = finite_max8(v);
-        if (mx > 0.f) atomicMax(&tok_max[t], __float_as_uint(mx));
+    for (int base = 0; base < count; base += 256 * kB) {
+        float v[kB][8];
+        load_batch(base, v);
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+            const float mx = finite_max8(v[j]);
+            if (mx > 0.f) atomicMax(&tok_max[(base + tid + 256 * j) % kMoeMxTok], __float_as_uint(mx));
+        }
     }
     __syncthreads();
     uint4* out = xf + (size_t)chunk * steps * 64;
-    for (int idx = tid; idx < count; idx += 256) {
-        int t, gg, st;
-        float v[8];
-        load8(idx, t, gg, st, v);
-        uint4 h, l;
-        split8(v, norm_exp(__uint_as_float(tok_max[t])), h, l);
-        out[(st * 4 + gg) * 16 + 2 * t] = h;
-        out[(st * 4 + gg) * 16 + 2 * t + 1] = l;
+    for (int base = 0; base < count; base += 256 * kB) {
+        float v[kB][8];
+        load_batch(base, v);
+#pragma unroll
+        for (int j = 0; j < kB; ++j) {
+            const int idx = base + tid + 256 * j;
+            if (idx >= count) continue;
+            const int t = idx % kMoeMxTok, gg = (idx / kMoeMxTok) & 3, st = idx / (4 * kMoeMxTok);
+            uint4 h, l;
+            split8(v[j], norm_exp(__uint_as_float(tok_max[t])), h, l);
+            out[(st * 4 + gg) * 16 + 2 * t] = h;
+            out[(st * 4 + gg) * 16 + 2 * t + 1] = l;
+        }
     }
     if (tid < kMoeMxTok) xe[chunk * kMoeMxTok + tid] = norm_exp(__uint_as_float(tok_max[tid]));
 }
@@ -1216,9 +1298,10 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
         hipLaunchKernelGGL(moe_router_route_kernel, dim3((unsigned)((E + 3) / 4), (unsigned)batch), dim3(256), 0,
                            stream, ra, static_cast<unsigned int*>(ws->arrive) + 1);
     } else {
-        hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)E, (unsigned)batch), dim3(64), 0, stream,
-                           L.router_type, static_cast<const uint8_t*>(L.router), (unsigned long long)rr, (int)E,
-                           (int)H, gr.bs, gr.bpb, X, (unsigned long long)ldx, logits, mags);
+        hipLaunchKernelGGL(moe_router_kernel, dim3((unsigned)((E + 3) / 4), (unsigned)((batch + kMoeRouterTok - 1) / kMoeRouterTok)),
+                           dim3(256), 0, stream, L.router_type, static_cast<const uint8_t*>(L.router),
+                           (unsigned long long)rr, (int)E, (int)H, gr.bs, gr.bpb, X, (unsigned long long)ldx,
+                           (int)batch, logits, mags);
         if (hipGetLastError() != hipSuccess) return -4;
         hipLaunchKernelGGL(moe_route_kernel, dim3((unsigned)batch), dim3(256), 0, stream, ra);
     }
