@@ -446,9 +446,10 @@ def bench_lm_head(torch, np, quantize, lib, stream, sptr, device):
             "bytes_per_token": p.nbytes,
             "roofline": roofline_hbm(p.nbytes, avg, load_traffic("traffic_configs", "lm_head_matvec"),
                                      kernel="mv_kernel (VALU) Q6_K batch 1, the logits matvec", timing=TIMING),
-            "roofline_with_id": roofline_hbm(p.nbytes, dt_head, None,
-                                             kernel="bound matvec + lm_argmax_kernel per token",
-                                             timing="graph replay per token, both launches and the gap between")}
+            "roofline_with_id": roofline_hbm(p.nbytes, dt_head, load_traffic("traffic_configs", "lm_head_with_id"),
+                                             kernel="lm_fused_kernel per token (bound matvec; its last "
+                                                    "workgroup decides the exact id)",
+                                             timing="graph replay per token (the launch and the gap to the next)")}
 
 
 def bench_moe(torch, np, quantize, stream, device, distinct_experts: int = 8):
@@ -486,7 +487,7 @@ def bench_moe(torch, np, quantize, stream, device, distinct_experts: int = 8):
                             "distinct_experts": round(float(np.mean(distinct)), 2),
                             "gbs": round(nbytes / dt / 1e9, 1),
                             "pct_hbm_peak": round(100 * nbytes / dt / 1e9 / HBM_PEAK_GBS, 2),
-                            "roofline": roofline_hbm(nbytes, dt, None,
+                            "roofline": roofline_hbm(nbytes, dt, load_traffic("traffic_configs", f"moe_b{batch}"),
                                                      kernel="router, routing, gate/up, down and combine launches",
                                                      timing="graph replay per layer call (all launches and the "
                                                             "gaps between them); bytes = router + the distinct "
@@ -552,7 +553,8 @@ def bench_llama_prefill(torch, np, stream, lib, sptr, mats):
                           "roofline": {"bound": "mfma", "achieved": round(fd / avg[dom] / 1e12, 1),
                                        "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                                        "frac": round(fd / avg[dom] / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
-                                       "traffic": None, "kernel": f"mg_kernel (MFMA dequant-GEMM) {dom} launch",
+                                       "traffic": load_traffic("traffic_configs", f"prefill_{dom}"),
+                                       "kernel": f"mg_kernel (MFMA dequant-GEMM) {dom} launch",
                                        "flops_per_launch": fd, "avg_launch_us": round(avg[dom] * 1e6, 2),
                                        "timing": TIMING}}
     del copies, arrs, xs, ys
@@ -578,7 +580,7 @@ def bench_llama_singles(torch, np, stream, device, lib, sptr, mats):
         singles[f"{name} {rows}x{cols} {label}"] = {
             "us": round(dt * 1e6, 2), "gbs": round(p.nbytes / dt / 1e9, 1),
             "pct_hbm_peak": round(100 * p.nbytes / dt / 1e9 / HBM_PEAK_GBS, 2),
-            "roofline": roofline_hbm(p.nbytes, avg1, load_traffic("traffic_llama_decode", name),
+            "roofline": roofline_hbm(p.nbytes, avg1, load_traffic("traffic_configs", f"single_{name}"),
                                      kernel=f"mv_kernel (VALU) {label} batch 1", timing=TIMING)}
         del ws1, first
     return singles
