@@ -520,6 +520,34 @@ static hipError_t mg_launch_tg(MgArgs& a, int tg, const float* X, unsigned long 
     return mg_launch_t<T, AL, 2>(a, X, ldx, s, e0, e1);
 }
 
+// Workgroups the GEMM launches would have for these matrices (one per
+// 256-row tile and token tile, sized as mg_group_launch sizes them).
+long long mg_workgroups(int type, const MatvecArgs* mats, size_t n, size_t batch) {
+    long long total = 0;
+    size_t i = 0;
+    while (i < n) {
+        size_t j = i + 1;
+        while (j < n && j - i < (size_t)kMgMaxMats && mats[j].x == mats[i].x && mats[j].ldx == mats[i].ldx &&
+               mats[j].cols == mats[i].cols)
+            ++j;
+        long long tiles = 0;
+        for (size_t k = i; k < j; ++k) tiles += (long long)((mats[k].rows + kMgRows - 1) / kMgRows);
+        int tg = 2;
+#define PYRITE_CASE(T) case T: tg = mg_tg_for<T>(tiles, batch); break;
+        switch (type) {
+            PYRITE_CASE(T_Q4_0) PYRITE_CASE(T_Q4_1) PYRITE_CASE(T_Q5_0) PYRITE_CASE(T_Q5_1)
+            PYRITE_CASE(T_Q8_0) PYRITE_CASE(T_Q8_1) PYRITE_CASE(T_Q2_K) PYRITE_CASE(T_Q3_K)
+            PYRITE_CASE(T_Q4_K) PYRITE_CASE(T_Q5_K) PYRITE_CASE(T_Q6_K) PYRITE_CASE(T_IQ4_NL)
+            PYRITE_CASE(T_IQ4_XS)
+        default: break;
+        }
+#undef PYRITE_CASE
+        total += tiles * (long long)((batch + 16 * tg - 1) / (16 * tg));
+        i = j;
+    }
+    return total;
+}
+
 // One launch set per run of consecutive matrices with the same activations
 // and columns (at most kMgMaxMats each).
 int mg_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, bool al, hipStream_t stream,

@@ -1,15 +1,18 @@
-// MFMA dequant-matvec for the GGML block formats (batch 1..8), gfx950.
+// MFMA dequant-matvec for the GGML block formats (batch 3 and up), gfx950.
 // Fragment construction and block formats: mx_traits.h.
 //
 // Schedule: a workgroup (4 waves) owns a task = a 32-row tile of one matrix
-// and a K part.  It first issues every load of the task at once: its
-// activations (unless already staged) and the tile's weight bytes of the part
-// as 16-byte buffer loads (coalesced, bounds-checked by the buffer range so
-// rows past the matrix read as zero), then parks the weights in LDS and
-// converts the activations into fp16 hi/lo A fragments in LDS.  Its waves
-// then split the part's blocks round-robin, decode B fragments from LDS and
-// run the MFMAs; the 4 partial results are summed in LDS in a fixed order,
-// so results are deterministic.  K parts are sized so that a part's
+// and a K part.  It first issues every load of the task at once: its first
+// 8-token chunk's activations (unless already staged) and the tile's weight
+// bytes of the part as 16-byte buffer loads (coalesced, bounds-checked by the
+// buffer range so rows past the matrix read as zero), then parks the weights
+// in LDS and converts the activations into fp16 hi/lo A fragments in LDS.
+// Its waves then split the part's blocks round-robin, decode B fragments from
+// LDS and run the MFMAs; the 4 partial results are summed in LDS in a fixed
+// order, so results are deterministic.  Batches of more than 8 vectors run
+// every further 8-token chunk against the same parked weights (the next
+// chunk's activations loaded during the current chunk's MFMAs), so a launch
+// reads each weight byte once whatever the batch.  K parts are sized so that a part's
 // fragments and weights fit in LDS with two workgroups per CU; matrices with
 // more parts are combined by the last part to arrive (split K).
 #include <hip/hip_ext.h>
@@ -29,18 +32,18 @@ struct MxDesc {
     unsigned long long ldx;
     float* Y;
     unsigned long long ldy;
-    float* part;          // split-K partial sums [ksplit][tiles][32 rows][8 tokens]
+    float* part;          // split-K partial sums [nchunk][ksplit][tiles][32 rows][8 tokens]
     unsigned* counters;   // per-tile arrival counters; zero between launches
     int rows;
     int cols;
-    int batch;            // activation vectors (<= 8)
+    int batch;            // activation vectors
     int ksplit;           // K parts (workgroup tasks per 32-row tile)
     int kpart_steps;      // 32-column steps per K part (a multiple of the block's steps)
     int tiles;            // ceil(rows / 32)
     int task_begin;       // first task of this matrix; tasks = ksplit * tiles
     int nch;              // 16-byte chunks loaded per row and part
     int rs;               // LDS bytes per row of the staged weights
-    int pad;
+    int nchunk;           // 8-token chunks of the batch, all multiplied against the parked weights
 };
 
 constexpr int kMxMaxGroup = 16;
@@ -155,12 +158,15 @@ __global__ __launch_bounds__(256, 2) void mx_kernel(const MxGroup grp) {
         const int kb1 = (s1 / F::STEPS < nblk) ? s1 / F::STEPS : nblk;
         const int nch = d.nch, rs = d.rs;
 
-        // 1. activations of the part, unless this workgroup staged them last
-        const bool stage = mi != staged_mi || kp != staged_kp;
+        // 1. activations of the part's first token chunk, unless this
+        // workgroup staged them last (one chunk only)
+        const int nck = d.nchunk;
+        const bool stage = nck > 1 || mi != staged_mi || kp != staged_kp;
         float xv[XI][8];
-        if (stage) {
-            const bool tok_ok = xt < d.batch;
-            const float* xp = d.X + (unsigned long long)(tok_ok ? xt : 0) * d.ldx;
+        auto load_x = [&](int c) {  // tokens NT c .. NT c + NT - 1
+            const int tok = NT * c + xt;
+            const bool tok_ok = tok < d.batch;
+            const float* xp = d.X + (unsigned long long)(tok_ok ? tok : 0) * d.ldx;
 #pragma unroll
             for (int k = 0; k < XI; ++k) {
                 const int s = s0 + xs + SPI * k;
@@ -174,7 +180,8 @@ __global__ __launch_bounds__(256, 2) void mx_kernel(const MxGroup grp) {
                     for (int i = 0; i < 8; ++i) xv[k][i] = 0.f;
                 }
             }
-        }
+        };
+        if (stage) load_x(0);
 
         // 2. the tile's weight bytes of the part: row r's chunk c is the 16
         // bytes at (its part start rounded down to 16) + 16 c.  The buffer
@@ -203,92 +210,107 @@ __global__ __launch_bounds__(256, 2) void mx_kernel(const MxGroup grp) {
             wv[k] = make_uint4(v.x, v.y, v.z, v.w);
         }
 
-        // 3. build the A fragments, then park the weights: the activations
-        // were loaded first and arrive first, so the fragments are built
-        // while the weight loads are still in flight
         lds_barrier();  // the previous task's fragments, weights and partials are consumed
-        if (stage) {
-            // Each token is staged scaled by the power of two 2^-e that brings
-            // its largest finite |x| into [2^14, 2^15) (see norm_exp); results
-            // are multiplied back by 2^e (exact).  A thread's items all belong
-            // to token xt.
-            float mx = 0.f;
-#pragma unroll
-            for (int k = 0; k < XI; ++k) mx = fmaxf(mx, finite_max8(xv[k]));
-            tb ^= 1;
-            if (tid < 8) tok_max[tb ^ 1][tid] = 0u;
-            if (mx > 0.f) atomicMax(&tok_max[tb][xt], __float_as_uint(mx));
-            lds_barrier();
-            const int e = norm_exp(__uint_as_float(tok_max[tb][xt]));
-#pragma unroll
-            for (int k = 0; k < XI; ++k) {
-                const int s = xs + SPI * k;
-                if (s0 + s < s1) {
-                    uint4 hi, lo;
-                    split8(xv[k], e, hi, lo);
-                    uint4* f = frag + (s * 4 + xg) * MB + 2 * xt;
-                    f[0] = hi;
-                    f[1] = lo;
-                }
-            }
-            staged_mi = mi;
-            staged_kp = kp;
-        }
-#pragma unroll
-        for (int k = 0; k < WI; ++k) {
-            const int c = tid + 256 * k;
-            const int r = c / nch, col = c - r * nch;
-            if (r < 32) *reinterpret_cast<uint4*>(wlds + r * rs + 16 * col) = wv[k];
-        }
-        lds_barrier();
-
-        // 4. this wave's blocks: rows n and n + 16 of the tile
         const uint8_t* p0 = wlds + n * rs + ((part0 + (unsigned)n * (unsigned)d.row_bytes) & 15u);
         const uint8_t* p1 = wlds + (n + 16) * rs + ((part0 + (unsigned)(n + 16) * (unsigned)d.row_bytes) & 15u);
-        f4v acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-        for (int b = kb0 + w; b < kb1; b += 4) {
-            typename F::Raw ra, rb;
-            F::template load<AL, true>(p0 + (b - kb0) * F::BPB, g, ra);
-            F::template load<AL, true>(p1 + (b - kb0) * F::BPB, g, rb);
-            mx_block<T, MB>(ra, rb, frag + (b * F::STEPS - s0) * 4 * MB, g, n, acc);
-        }
-
-        // Sum the 4 waves' partials in a fixed order.  Lane (n, g) of wave w
-        // holds rows r0 / r1 and token-parts 4g..4g+3 = tokens 2g and 2g+1 (hi, lo).
-        float* rw = red + (w * 2 * 64 + lane) * 4;
-        *reinterpret_cast<f4v*>(rw) = acc[0];
-        *reinterpret_cast<f4v*>(rw + 64 * 4) = acc[1];
-        lds_barrier();
         const int rt = tid >> 7, t = (tid >> 4) & 7, nn = tid & 15;
-        float sum;
-        {
-            const int src = ((t >> 1) << 4) | nn, j = (t & 1) * 2;
-            sum = 0.f;
-#pragma unroll
-            for (int ww = 0; ww < 4; ++ww) {
-                const float* q = red + ((ww * 2 + rt) * 64 + src) * 4;
-                sum += q[j] + q[j + 1];
-            }
-            sum = __builtin_amdgcn_ldexpf(sum, norm_exp(__uint_as_float(tok_max[tb][t])));
-        }
         const int trow = rt * 16 + nn;
         const long long row = (long long)tile * 32 + trow;
-        if (d.ksplit == 1) {
-            if (t < d.batch && row < rows) d.Y[t * d.ldy + row] = sum;
-        } else {
-            // split K: publish this part; the last part to arrive sums all parts
-            // in part order (deterministic) and writes y, then re-arms the
-            // counter (device-coherent hand-off, see st_dev / arrive_dev).
-            float* pt = d.part + ((size_t)kp * d.tiles + tile) * 256;
-            st_dev(pt + trow * 8 + t, sum);
+        // every token chunk against the weights parked once: the weights are
+        // read from HBM once per launch whatever the batch
+        for (int c = 0; c < nck; ++c) {
+            // 3. build the A fragments (the first chunk's while the weight
+            // loads are still in flight), then park the weights
+            if (stage) {
+                // Each token is staged scaled by the power of two 2^-e that brings
+                // its largest finite |x| into [2^14, 2^15) (see norm_exp); results
+                // are multiplied back by 2^e (exact).  A thread's items all belong
+                // to token xt of the chunk.
+                float mx = 0.f;
+#pragma unroll
+                for (int k = 0; k < XI; ++k) mx = fmaxf(mx, finite_max8(xv[k]));
+                tb ^= 1;
+                if (tid < 8) tok_max[tb ^ 1][tid] = 0u;
+                if (mx > 0.f) atomicMax(&tok_max[tb][xt], __float_as_uint(mx));
+                lds_barrier();
+                const int e = norm_exp(__uint_as_float(tok_max[tb][xt]));
+#pragma unroll
+                for (int k = 0; k < XI; ++k) {
+                    const int s = xs + SPI * k;
+                    if (s0 + s < s1) {
+                        uint4 hi, lo;
+                        split8(xv[k], e, hi, lo);
+                        uint4* f = frag + (s * 4 + xg) * MB + 2 * xt;
+                        f[0] = hi;
+                        f[1] = lo;
+                    }
+                }
+            }
+            // the next chunk's activations, in flight during this chunk's MFMAs
+            if (c + 1 < nck) load_x(c + 1);
+            if (c == 0) {
+#pragma unroll
+                for (int k = 0; k < WI; ++k) {
+                    const int cc = tid + 256 * k;
+                    const int r = cc / nch, col = cc - r * nch;
+                    if (r < 32) *reinterpret_cast<uint4*>(wlds + r * rs + 16 * col) = wv[k];
+                }
+            }
+            lds_barrier();
+
+            // 4. this wave's blocks: rows n and n + 16 of the tile
+            f4v acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+            for (int b = kb0 + w; b < kb1; b += 4) {
+                typename F::Raw ra, rb;
+                F::template load<AL, true>(p0 + (b - kb0) * F::BPB, g, ra);
+                F::template load<AL, true>(p1 + (b - kb0) * F::BPB, g, rb);
+                mx_block<T, MB>(ra, rb, frag + (b * F::STEPS - s0) * 4 * MB, g, n, acc);
+            }
+
+            // Sum the 4 waves' partials in a fixed order.  Lane (n, g) of wave w
+            // holds rows r0 / r1 and token-parts 4g..4g+3 = tokens 2g and 2g+1 (hi, lo).
+            float* rw = red + (w * 2 * 64 + lane) * 4;
+            *reinterpret_cast<f4v*>(rw) = acc[0];
+            *reinterpret_cast<f4v*>(rw + 64 * 4) = acc[1];
+            lds_barrier();
+            float sum;
+            {
+                const int src = ((t >> 1) << 4) | nn, j = (t & 1) * 2;
+                sum = 0.f;
+#pragma unroll
+                for (int ww = 0; ww < 4; ++ww) {
+                    const float* q = red + ((ww * 2 + rt) * 64 + src) * 4;
+                    sum += q[j] + q[j + 1];
+                }
+                sum = __builtin_amdgcn_ldexpf(sum, norm_exp(__uint_as_float(tok_max[tb][t])));
+            }
+            const int tok = NT * c + t;
+            if (d.ksplit == 1) {
+                if (t < NT && tok < d.batch && row < rows) d.Y[tok * d.ldy + row] = sum;
+            } else {
+                st_dev(d.part + (((size_t)c * d.ksplit + kp) * d.tiles + tile) * 256 + trow * 8 + t, sum);
+            }
+            if (c + 1 < nck) lds_barrier();  // fragments and partials consumed before the next chunk
+        }
+        staged_mi = nck > 1 ? -1 : mi;
+        staged_kp = kp;
+        if (d.ksplit > 1) {
+            // split K: every chunk of this part is published; the last part to
+            // arrive sums all parts in part order (deterministic) and writes y,
+            // then re-arms the counter (device-coherent hand-off, see st_dev /
+            // arrive_dev)
             drain_dev();
             __syncthreads();
             if (tid == 0) last_flag = arrive_dev(&d.counters[tile]) == (unsigned)(d.ksplit - 1);
             __syncthreads();
             if (last_flag) {
-                float tot = 0.f;
-                for (int k = 0; k < d.ksplit; ++k) tot += ld_dev(d.part + ((size_t)k * d.tiles + tile) * 256 + trow * 8 + t);
-                if (t < d.batch && row < rows) d.Y[t * d.ldy + row] = tot;
+                for (int c = 0; c < nck; ++c) {
+                    float tot = 0.f;
+                    for (int k = 0; k < d.ksplit; ++k)
+                        tot += ld_dev(d.part + (((size_t)c * d.ksplit + k) * d.tiles + tile) * 256 + trow * 8 + t);
+                    const int tok = NT * c + t;
+                    if (t < NT && tok < d.batch && row < rows) d.Y[tok * d.ldy + row] = tot;
+                }
                 if (tid == 0) st_dev(&d.counters[tile], 0u);
             }
         }
@@ -341,7 +363,7 @@ static MxPlanOut mx_plan(MxGroup& grp) {
         d.task_begin = (int)out.tasks;
         out.tasks += (long long)d.ksplit * d.tiles;
         if (d.ksplit > 1) {
-            out.part_floats += (size_t)d.ksplit * d.tiles * 256;
+            out.part_floats += (size_t)d.nchunk * d.ksplit * d.tiles * 256;
             out.counters += d.tiles;
         }
         if (d.kpart_steps > out.max_kps) out.max_kps = d.kpart_steps;
@@ -393,7 +415,7 @@ static hipError_t mx_launch_group(MxGroup& grp, hipStream_t stream, hipEvent_t s
             if (d.ksplit > 1) {
                 d.part = part + po;
                 d.counters = ctr + co;
-                po += (size_t)d.ksplit * d.tiles * 256;
+                po += (size_t)d.nchunk * d.ksplit * d.tiles * 256;
                 co += d.tiles;
             } else {
                 d.part = nullptr;
@@ -438,8 +460,9 @@ bool mx_type_supported(int type) {
     }
 }
 
-// Launch the MFMA path for up to 8 activation vectors starting at vector
-// `done` of each matrix; arguments already validated.
+// Launch the MFMA path for the activation vectors from vector `done` of each
+// matrix on (up to 8 per 8-token chunk, every chunk in the same launch, so
+// each weight is read once); arguments already validated.
 int mx_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, size_t done, bool al,
                     hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     const TypeGeo geo = type_geo(type);
@@ -458,6 +481,7 @@ int mx_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, si
             d.rows = (int)m.rows;
             d.cols = (int)m.cols;
             d.batch = (int)batch;
+            d.nchunk = batch > 8 ? (int)((batch + 7) / 8) : 1;
             d.part = nullptr;
             d.counters = nullptr;
         }

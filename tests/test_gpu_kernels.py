@@ -311,30 +311,38 @@ def test_device_matvec_activation_scales(torch_dev, t, batch):
         assert_matvec_close(y[b], ref, xs[b], rowmax, f"{TYPES[t][0]} scale {scales[b]:g} b{b}/{batch}")
 
 
-@pytest.mark.parametrize("batch", [64, 100])
+@pytest.mark.parametrize("batch", [64, 100, 130])
 @pytest.mark.parametrize("t", QUANT_TYPES, ids=lambda t: TYPES[t][0])
 def test_device_matvec_gemm_batches(torch_dev, t, batch):
-    """Prefill-sized batches (the MFMA dequant-GEMM for the block formats it
-    covers): ragged row and token tiles, every vector checked."""
+    """Batches of 64-130 vectors of a 150-row matrix: the dispatcher's cost
+    estimate sends 64 vectors of the super-block formats other than Q4_K to
+    the chunked MFMA matvec (eight 8-token chunks against weights read once)
+    and the rest to the MFMA dequant-GEMM; ragged row and token tiles, every
+    vector checked."""
     announce("device_matvec_gemm", TYPES[t][0], 150, 1024, batch)
     _device_matvec_check(torch_dev, t, 150, 1024, batch, seed=9500 + t)
 
 
 @pytest.mark.parametrize("t,rows,cols,batch", [(12, 4096, 4096, 96), (14, 4096, 4096, 64), (8, 1024, 14336, 72),
-                                               (12, 14336, 4096, 33)])
+                                               (12, 14336, 4096, 33), (12, 14336, 4096, 64), (14, 4096, 4096, 128)])
 def test_device_matvec_gemm_llama_shapes(torch_dev, t, rows, cols, batch):
-    """Llama-3-8B projection shapes at prefill batch sizes."""
+    """Llama-3-8B projection shapes at batches from 33 to 128, on whichever of
+    the chunked MFMA matvec and the dequant-GEMM the dispatcher estimates
+    faster (Q6_K 4096x4096 at 64 and Q8_0 1024x14336 at 72 take the matvec,
+    the others the GEMM)."""
     announce("device_matvec_gemm_llama", TYPES[t][0], rows, cols, batch)
     _device_matvec_check(torch_dev, t, rows, cols, batch, seed=9600 + rows + t)
 
 
+@pytest.mark.parametrize("batch", [40, 112])
 @pytest.mark.parametrize("t", [12, 14], ids=lambda t: TYPES[t][0])
-def test_device_matvec_random_payloads_gemm(torch_dev, t):
+def test_device_matvec_random_payloads_gemm(torch_dev, t, batch):
+    """Random block bytes at 40 vectors (chunked MFMA matvec) and 112 (GEMM)."""
     torch = torch_dev
     from pyrite_amd import device
 
     o = oracle()
-    rows, cols, batch = 70, 1024, 80
+    rows, cols = 70, 1024
     payload = _random_payload(t, rows, cols, 4400 + t)
     announce("device_matvec_random_gemm", TYPES[t][0], rows, cols, batch)
     xs = np.stack([o.normal(4500 + b, cols) for b in range(batch)]).astype(np.float32)
