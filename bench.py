@@ -523,12 +523,38 @@ LLAMA_WORKLOAD = ("Llama-3-8B layer, Q4_K_M mix: q/o 4096x4096, k/v 1024x4096, g
 
 
 def bench_llama(torch, np, quantize, stream, device, lib, sptr, mats):
-    """Llama-3-8B layer in Q4_K_M mix: its q, gate and down matrices alone at batch 1,
-    and the 512-token prefill (four launches, MFMA dequant-GEMM)."""
+    """Llama-3-8B layer in Q4_K_M mix: its q, gate and down matrices alone at batch 1
+    and at 8-96 vectors, and the 512-token prefill (four launches, MFMA dequant-GEMM)."""
     res = {"workload": LLAMA_WORKLOAD, "bytes_per_layer": sum(p.nbytes for _, _, _, p in mats.values())}
     res["prefill_512"] = bench_llama_prefill(torch, np, stream, lib, sptr, mats)
     res["decode_b1_matrices"] = bench_llama_singles(torch, np, stream, device, lib, sptr, mats)
+    res["multi_vector_matrices"] = bench_llama_batches(torch, np, stream, device, mats)
     return res
+
+
+def bench_llama_batches(torch, np, stream, device, mats, batches=(8, 16, 32, 48, 63, 96)):
+    """The layer's q, gate and down matrices at several vectors per call (batched decode
+    of that many sequences), over rotated copies beyond the Infinity Cache: the MFMA
+    matvec (each weight read once for all the 8-token chunks) or the dequant-GEMM,
+    whichever the library's estimate picks for the matrix and batch."""
+    out = {}
+    for name in ("q", "gate", "down"):
+        t, rows, cols, p = mats[name]
+        n = max(2, int(np.ceil(600e6 / p.nbytes)))
+        first = torch.from_numpy(p).cuda()
+        ws = [first] + [first.clone() for _ in range(n - 1)]
+        label = {12: "Q4_K", 14: "Q6_K"}[t]
+        per = {}
+        for b in batches:
+            x = torch.randn(b, cols, device="cuda")
+            y = torch.empty(b, rows, device="cuda")
+            dt = time_graph(torch, stream, [lambda w=w: device.matvec(t, w, x, rows, cols, out=y) for w in ws * 2])
+            per[f"b{b}"] = {"us": round(dt * 1e6, 2), "weight_gbs": round(p.nbytes / dt / 1e9, 1),
+                            "vectors_per_s": round(b / dt, 1)}
+        out[f"{name} {rows}x{cols} {label}"] = per
+        del ws, first
+        torch.cuda.empty_cache()
+    return out
 
 
 def bench_llama_prefill(torch, np, stream, lib, sptr, mats):
