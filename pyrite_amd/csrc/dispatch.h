@@ -73,7 +73,7 @@ int mx_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, si
 
 // mg.hip: MFMA dequant-GEMM for large batches (arguments already validated);
 // consecutive matrices with the same activations share a launch.
-long long mg_workgroups(int type, const MatvecArgs* mats, size_t n, size_t batch);
+long long mg_workgroups(int type, const MatvecArgs* mats, size_t n, size_t batch, int* kblocks);
 int mg_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, bool al, hipStream_t stream,
                     hipEvent_t start, hipEvent_t stop);
 

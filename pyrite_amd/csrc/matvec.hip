@@ -12,27 +12,27 @@ namespace pyrite {
 // dequant-GEMM and the chunked MFMA matvec this estimate makes faster (us;
 // constants fitted to MI355X timings of 2048x1024 Q3_K, 14336x4096 Q4_K and
 // 4096x14336 Q6_K at 16-128 vectors):
-//   GEMM:   10 + (3.2 for Q4_K, 4.8 otherwise) x blocks per row, per pass of
-//           up to 256 workgroups (it has no K split, so a launch of few row
-//           tiles runs its blocks serially: 4096x14336 Q6_K takes 267 us at
-//           64 vectors on 32 workgroups);
+//   GEMM:   10 (+ 6 for the reduce launch of a split-K launch) + (3.2 for
+//           Q4_K, 4.8 otherwise) x the blocks one workgroup walks (a row's
+//           blocks, or its K part's when the launch splits K to fill the
+//           CUs), per pass of up to 256 workgroups;
 //   matvec: 5 + per 8-token chunk max(3, weight bytes / 2 TB/s) (weights
 //           read once, each chunk's MFMAs over the parked weights).
 constexpr size_t kGemmMinBatch = 16;
 
 static bool gemm_faster(int type, const TypeGeo& g, const MatvecArgs* mats, size_t n, size_t batch) {
     if (batch < kGemmMinBatch) return false;
-    size_t max_blk = 0;
+    size_t max_cols = 0;
+    for (size_t i = 0; i < n; ++i)
+        if (mats[i].cols > max_cols) max_cols = mats[i].cols;
     double bytes = 0.0;
-    for (size_t i = 0; i < n; ++i) {
-        const size_t nb = mats[i].cols / g.bs;
-        if (nb > max_blk) max_blk = nb;
-        bytes += (double)mats[i].rows * (double)(nb * g.bpb);
-    }
+    for (size_t i = 0; i < n; ++i) bytes += (double)mats[i].rows * (double)(mats[i].cols / g.bs * g.bpb);
     // per-block cost in units of one 256-column super-block
     const double per_blk = (type == T_Q4_K ? 3.2 : 4.8) * (double)g.bs / 256.0;
-    const long long wgs = mg_workgroups(type, mats, n, batch);
-    const double t_gemm = 10.0 + per_blk * (double)max_blk * (double)((wgs + 255) / 256);
+    int kblocks = 0;
+    const long long wgs = mg_workgroups(type, mats, n, batch, &kblocks);
+    const bool split = kblocks * g.bs < (int)(max_cols);
+    const double t_gemm = 10.0 + (split ? 6.0 : 0.0) + per_blk * (double)kblocks * (double)((wgs + 255) / 256);
     const double chunk = bytes / 2e6 > 3.0 ? bytes / 2e6 : 3.0;
     const double t_mx = 5.0 + chunk * (double)((batch + 7) / 8);
     return t_gemm < t_mx;

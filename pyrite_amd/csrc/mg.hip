@@ -85,6 +85,9 @@ struct MgArgs {
     int Gp;  // 16-token groups per fragment step in XF (token tiles * TG)
     int cols, batch;
     int row_tiles, tok_tiles;
+    int ksplit, kblocks;  // K parts and blocks per part (split K when the tiles alone leave CUs idle)
+    int reduce;           // 1: the launch after a split-K launch, summing its parts into y
+    float* part;          // [ksplit][row_tiles * tok_tiles][512 threads][TG * 2 * 4] partial sums
 };
 
 // ---------------------------------------------------------------- activations
@@ -242,10 +245,12 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
     // XCD-aware order: workgroup b runs on XCD b % 8; logical tile L counts
     // each XCD's workgroups contiguously, so the token tiles of a row tile
     // share an XCD and run next to each other.
-    const int N = a.row_tiles * a.tok_tiles;
+    const int N = a.row_tiles * a.tok_tiles * (a.reduce ? 1 : a.ksplit);
     const int bx = blockIdx.x, xcd = bx & 7, per = N >> 3, rem = N & 7;
     const int L = xcd * per + (xcd < rem ? xcd : rem) + (bx >> 3);
-    const int rt = L / a.tok_tiles, tt = L - rt * a.tok_tiles;
+    // K part outermost: the workgroups of one part and row tile stay adjacent
+    const int kp = L / (a.row_tiles * a.tok_tiles), Lt = L - kp * (a.row_tiles * a.tok_tiles);
+    const int rt = Lt / a.tok_tiles, tt = Lt - rt * a.tok_tiles;
 
     // matrix of this row tile (workgroup-uniform)
     const uint8_t* W = a.m[0].W;
@@ -273,16 +278,64 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
         const long long r = rbase + 16 * i;
         rp[i] = W + (r < rows ? r : rows - 1) * row_bytes;
     }
-    const int nblk = a.cols / F::BS;
+    // D rows 4g..4g+3 = tokens 4g..4g+3 of each group
+    auto write_out = [&](auto value) {  // value(f, i, k): the (token, row) sum before scaling
+#pragma unroll
+        for (int f = 0; f < TG; ++f) {
+            const int t0 = (tt * TG + f) * 16 + 4 * g;
+            int ex[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) ex[k] = t0 + k < a.batch ? a.texp[t0 + k] : 0;
+#pragma unroll
+            for (int i = 0; i < NT; ++i) {
+                const long long row = rbase + 16 * i;
+                if (row >= rows) continue;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (t0 + k < a.batch)
+                        Y[(unsigned long long)(t0 + k) * ldy + row] = __builtin_amdgcn_ldexpf(value(f, i, k), ex[k]);
+            }
+        }
+    };
+    // Split K: a part's sums go to the part buffer with plain stores (thread
+    // tid's TG x NT x 4 values, 16 bytes per (group, tile)); the launch after
+    // it (reduce mode, one workgroup per tile) adds the parts in part order
+    // (deterministic) and writes y.
+    constexpr int PE = TG * NT * 4;
+    const size_t ntile = (size_t)a.row_tiles * a.tok_tiles;
+    const size_t pstride = ntile * (kMgWaves * 64) * PE;  // floats per K part
+    if (a.reduce) {
+        const float* col0 = a.part + ((size_t)Lt * (kMgWaves * 64) + tid) * PE;
+        f4v tot[TG][NT];
+#pragma unroll
+        for (int f = 0; f < TG; ++f)
+#pragma unroll
+            for (int i = 0; i < NT; ++i) tot[f][i] = f4v{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < a.ksplit; ++q) {
+#pragma unroll
+            for (int f = 0; f < TG; ++f)
+#pragma unroll
+                for (int i = 0; i < NT; ++i)
+                    tot[f][i] += *reinterpret_cast<const f4v*>(col0 + (size_t)q * pstride + (f * NT + i) * 4);
+        }
+        write_out([&](int f, int i, int k) { return tot[f][i][k]; });
+        return;
+    }
+
+    // this workgroup's K blocks [blo, bhi)
+    const int nblk_all = a.cols / F::BS;
+    const int blo = kp * a.kblocks;
+    const int bhi = blo + a.kblocks < nblk_all ? blo + a.kblocks : nblk_all;
+    const int nblk = bhi - blo;
     const int nchunk = (nblk + BPC - 1) / BPC;
-    const int nxs = nblk * XPB;
+    const int nxs = bhi * XPB;
     // this workgroup's groups are contiguous in each fragment step
     const uint4* xsrc = a.XF + (size_t)tt * FS * 64 + lane;
 
     // the chunk's fragments: fragment j = (fragment step j / FS, group and part j % FS)
     constexpr int KPW = (CF + kMgWaves - 1) / kMgWaves;  // copies per wave and chunk
     auto stage_k = [&](int ch, int buf, int k) {
-        const int x0 = ch * CX;
+        const int x0 = blo * XPB + ch * CX;
         const int nx = nxs - x0 < CX ? nxs - x0 : CX;
         const int j = w + kMgWaves * k;
         const int xl = j / FS, fl = j - xl * FS;
@@ -314,10 +367,10 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
 
     typename F::Raw ca[NT], na[NT];
     if constexpr (WL) {
-        wstage(0);
+        wstage(blo);
     } else {
 #pragma unroll
-        for (int i = 0; i < NT; ++i) F::template load<AL, false, UA>(rp[i], g, ca[i]);
+        for (int i = 0; i < NT; ++i) F::template load<AL, false, UA>(rp[i] + (size_t)blo * F::BPB, g, ca[i]);
     }
     stage(0, 0);
 
@@ -334,17 +387,17 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
         __syncthreads();
         if (ch + 1 < nchunk) stage(ch + 1, (ch + 1) & 1);
         const uint4* ab = abuf[ch & 1] + lane;
-        const int b0 = ch * BPC;
-        const int b1 = b0 + BPC < nblk ? b0 + BPC : nblk;
+        const int b0 = blo + ch * BPC;
+        const int b1 = b0 + BPC < bhi ? b0 + BPC : bhi;
         for (int b = b0; b < b1; ++b) {
-            const int bn = b + 1 < nblk ? b + 1 : nblk - 1;
+            const int bn = b + 1 < bhi ? b + 1 : bhi - 1;
             if constexpr (WL) {
                 // this block's spans out of the wave's region (landed: the
                 // chunk began with vmcnt(0)), then the next block into it
 #pragma unroll
                 for (int i = 0; i < NT; ++i) F::template load<false, true>(wrow(i, b), g, ca[i]);
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                if (b + 1 < nblk) wstage(b + 1);
+                if (b + 1 < bhi) wstage(b + 1);
             } else {
 #pragma unroll
                 for (int i = 0; i < NT; ++i)
@@ -442,23 +495,15 @@ __global__ __launch_bounds__(kMgWaves * 64) void mg_kernel(const MgArgs a) {
         }
     }
 
-    // D rows 4g..4g+3 = tokens 4g..4g+3 of each group
-#pragma unroll
-    for (int f = 0; f < TG; ++f) {
-        const int t0 = (tt * TG + f) * 16 + 4 * g;
-        int ex[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) ex[k] = t0 + k < a.batch ? a.texp[t0 + k] : 0;
-#pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            const long long row = rbase + 16 * i;
-            if (row >= rows) continue;
-            const f4v v = acc[f][i];
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (t0 + k < a.batch) Y[(unsigned long long)(t0 + k) * ldy + row] = __builtin_amdgcn_ldexpf(v[k], ex[k]);
-        }
+    if (a.ksplit == 1) {
+        write_out([&](int f, int i, int k) { return acc[f][i][k]; });
+        return;
     }
+    float* mine = a.part + (size_t)kp * pstride + ((size_t)Lt * (kMgWaves * 64) + tid) * PE;
+#pragma unroll
+    for (int f = 0; f < TG; ++f)
+#pragma unroll
+        for (int i = 0; i < NT; ++i) *reinterpret_cast<f4v*>(mine + (f * NT + i) * 4) = acc[f][i];
 }
 
 // ---------------------------------------------------------------- launch
@@ -470,6 +515,31 @@ struct MgWorkspace {
     size_t cap = 0;  // bytes
 };
 static MgWorkspace g_mg_ws[64];
+// Split-K partial sums, one buffer per device; launches that split K on one
+// device must be ordered on one stream.
+static MgWorkspace g_mg_part[64];
+
+// K parts of a launch whose tiles alone give `tiles` workgroups.  A launch of
+// fewer than 192 tiles (under a pass over the 256 CUs) is split into the part
+// count that minimises passes x blocks per part (one block added for
+// the partial sums and their reduce launch), each part at least one staging
+// chunk (bpc blocks) and two blocks long; larger launches are not split.
+static void mg_split(long long tiles, int nblk, int bpc, int* ksplit, int* kblocks) {
+    *ksplit = 1;
+    *kblocks = nblk;
+    if (tiles >= 192 || tiles < 1) return;
+    const int kmin = bpc > 2 ? bpc : 2;
+    long long best = nblk;  // one pass, whole rows
+    for (int ks = 2; ks <= 64 && (nblk + ks - 1) / ks >= kmin; ++ks) {
+        const int kb = (nblk + ks - 1) / ks, parts = (nblk + kb - 1) / kb;
+        const long long cost = (tiles * parts + 255) / 256 * kb + 1;
+        if (cost < best) {
+            best = cost;
+            *ksplit = parts;
+            *kblocks = kb;
+        }
+    }
+}
 
 template <int T, bool AL, int TG>
 static hipError_t mg_launch_t(MgArgs& a, const float* X, unsigned long long ldx, hipStream_t s, hipEvent_t e0,
@@ -488,6 +558,15 @@ static hipError_t mg_launch_t(MgArgs& a, const float* X, unsigned long long ldx,
     int* texp = reinterpret_cast<int*>(static_cast<uint8_t*>(ws.block) + frag_bytes);
     a.XF = XF;
     a.texp = texp;
+    a.part = nullptr;
+    a.reduce = 0;
+    if (a.ksplit > 1) {
+        const size_t ntile = (size_t)a.row_tiles * a.tok_tiles;
+        const size_t pbytes = (size_t)a.ksplit * ntile * (kMgWaves * 64) * (TG * kMgWaveTiles * 4) * sizeof(float);
+        MgWorkspace& wp = g_mg_part[dev];
+        if (pbytes > wp.cap && (e = workspace_grow(&wp.block, &wp.cap, pbytes, false, s)) != hipSuccess) return e;
+        a.part = static_cast<float*>(wp.block);
+    }
     const dim3 gexp(a.batch), gfrag((unsigned)((long long)a.Gp * ((nsteps + 7) / 8)));
     if (e0)
         hipExtLaunchKernelGGL(mg_exp_kernel, gexp, dim3(256), 0, s, e0, nullptr, 0, X, ldx, a.cols, texp);
@@ -495,11 +574,21 @@ static hipError_t mg_launch_t(MgArgs& a, const float* X, unsigned long long ldx,
         hipLaunchKernelGGL(mg_exp_kernel, gexp, dim3(256), 0, s, X, ldx, a.cols, texp);
     hipLaunchKernelGGL((mg_frag_kernel<T>), gfrag, dim3(256), 0, s, X, ldx, a.cols, a.batch, (const int*)texp, XF,
                        a.Gp);
-    const unsigned wgs = (unsigned)((long long)a.row_tiles * a.tok_tiles);
-    if (e1)
-        hipExtLaunchKernelGGL((mg_kernel<T, AL, TG>), dim3(wgs), dim3(kMgWaves * 64), 0, s, nullptr, e1, 0, a);
+    const unsigned ntile = (unsigned)((long long)a.row_tiles * a.tok_tiles);
+    const unsigned wgs = ntile * (unsigned)a.ksplit;
+    hipEvent_t ec = a.ksplit > 1 ? nullptr : e1;  // the launch that ends the set records the stop event
+    if (ec)
+        hipExtLaunchKernelGGL((mg_kernel<T, AL, TG>), dim3(wgs), dim3(kMgWaves * 64), 0, s, nullptr, ec, 0, a);
     else
         hipLaunchKernelGGL((mg_kernel<T, AL, TG>), dim3(wgs), dim3(kMgWaves * 64), 0, s, a);
+    if (a.ksplit > 1) {
+        MgArgs r = a;
+        r.reduce = 1;
+        if (e1)
+            hipExtLaunchKernelGGL((mg_kernel<T, AL, TG>), dim3(ntile), dim3(kMgWaves * 64), 0, s, nullptr, e1, 0, r);
+        else
+            hipLaunchKernelGGL((mg_kernel<T, AL, TG>), dim3(ntile), dim3(kMgWaves * 64), 0, s, r);
+    }
     return hipGetLastError();
 }
 
@@ -521,9 +610,13 @@ static hipError_t mg_launch_tg(MgArgs& a, int tg, const float* X, unsigned long 
 }
 
 // Workgroups the GEMM launches would have for these matrices (one per
-// 256-row tile and token tile, sized as mg_group_launch sizes them).
-long long mg_workgroups(int type, const MatvecArgs* mats, size_t n, size_t batch) {
+// 256-row tile, token tile and K part, sized as mg_group_launch sizes them),
+// and the most blocks a workgroup walks (*kblocks).
+long long mg_workgroups(int type, const MatvecArgs* mats, size_t n, size_t batch, int* kblocks) {
+    const TypeGeo geo = type_geo(type);
+    const int bpc = geo.bs >= 256 ? 1 : 256 / geo.bs;
     long long total = 0;
+    *kblocks = 0;
     size_t i = 0;
     while (i < n) {
         size_t j = i + 1;
@@ -542,7 +635,11 @@ long long mg_workgroups(int type, const MatvecArgs* mats, size_t n, size_t batch
         default: break;
         }
 #undef PYRITE_CASE
-        total += tiles * (long long)((batch + 16 * tg - 1) / (16 * tg));
+        const long long wt = tiles * (long long)((batch + 16 * tg - 1) / (16 * tg));
+        int ks = 1, kb = 0;
+        mg_split(wt, (int)(mats[i].cols / geo.bs), bpc, &ks, &kb);
+        if (kb > *kblocks) *kblocks = kb;
+        total += wt * ks;
         i = j;
     }
     return total;
@@ -588,7 +685,9 @@ int mg_group_launch(int type, const MatvecArgs* mats, size_t n, size_t batch, bo
         a.row_tiles = (int)tiles;
         a.tok_tiles = (int)((batch + 16 * tg - 1) / (16 * tg));
         a.Gp = a.tok_tiles * tg;
-        if (tiles * a.tok_tiles > 0x7FFFFFFFLL || (long long)a.Gp * ((a.cols / 32 + 7) / 8) > 0x7FFFFFFFLL)
+        mg_split(tiles * a.tok_tiles, (int)(mats[i].cols / geo.bs), geo.bs >= 256 ? 1 : 256 / geo.bs, &a.ksplit,
+                 &a.kblocks);
+        if (tiles * a.tok_tiles * a.ksplit > 0x7FFFFFFFLL || (long long)a.Gp * ((a.cols / 32 + 7) / 8) > 0x7FFFFFFFLL)
             return -2;
         hipEvent_t e0 = i == 0 ? start : nullptr, e1 = j == n ? stop : nullptr;
         hipError_t e = hipSuccess;
