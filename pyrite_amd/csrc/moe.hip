@@ -204,9 +204,6 @@ __device__ double moe_ref_row_seq(int type, const uint8_t* rp, int H, int bs, in
 // ---------------------------------------------------------------- routing + plan
 
 struct MoePlan {
-    int* cnt;        // [E] pairs per expert
-    int* poff;       // [E + 1] padded pair offsets (chunks of MB)
-    int* coff;       // [E + 1] chunk offsets
     int* pair_tok;   // [max_pairs] token of each padded pair, -1 for padding
     int* pos;        // [batch * k] padded pair index of (token, slot)
     int* totals;     // [2]: padded pairs, chunks
@@ -453,25 +450,13 @@ __device__ void moe_route_token(const MoeRouteArgs& a, const int t) {
     //    each pair's results are computed independently of its chunk mates.
     const MoePlan& p = a.plan;
     if (a.batch == 1 && a.MB == 1) {
-        // One token, one pair per chunk: an expert's pair and chunk offsets
-        // are the number of chosen experts below it (the general path's
-        // result, without its buckets and scans; no padding).
-        for (int e = tid; e <= E; e += 256) {
-            int below = 0, hit = 0;
-            for (int j = 0; j < k; ++j) {
-                below += s_top[j] < e;
-                hit += s_top[j] == e;
-            }
-            p.poff[e] = below;
-            p.coff[e] = below;
-            if (e < E) p.cnt[e] = hit;
-        }
+        // One token, one pair per chunk, pairs in slot order (pair q is slot
+        // q, so the combine reads them without the position table).  The k
+        // experts are distinct, so no bucket holds two pairs.
         if (tid < k) {
-            int below = 0;
-            for (int j = 0; j < k; ++j) below += s_top[j] < s_top[tid];
-            p.pair_tok[below] = 0;
-            p.pos[tid] = below;
-            p.chunk_e[below] = s_top[tid];
+            p.pair_tok[tid] = 0;
+            p.pos[tid] = tid;
+            p.chunk_e[tid] = s_top[tid];
         }
         if (tid == 0) {
             p.totals[0] = k;
@@ -497,51 +482,38 @@ __device__ void moe_route_token(const MoeRouteArgs& a, const int t) {
     __syncthreads();
     for (int q = tid; q < npairs; q += 256) atomicAdd(&s_cnt[id_of(q)], 1);
     __syncthreads();
-    // exclusive prefix sums over experts of padded pairs and chunks: each
-    // thread scans 4 consecutive experts, then the 256 thread totals
+    // exclusive prefix sums over experts of padded pairs: each thread scans
+    // 4 consecutive experts, then the 256 thread totals
     {
         const int e0 = tid * 4;
-        int cp[4], cc[4], sp = 0, sc = 0;
+        int cp[4], sp = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int e = e0 + j;
             const int n = e < E ? s_cnt[e] : 0;
-            const int nc = (n + a.MB - 1) / a.MB;
             cp[j] = sp;
-            cc[j] = sc;
-            sp += nc * a.MB;
-            sc += nc;
+            sp += (n + a.MB - 1) / a.MB * a.MB;
         }
-        // inclusive scan of (sp, sc) across the wave
-        int ip = sp, ic = sc;
+        // inclusive scan across the wave
+        int ip = sp;
         for (int off = 1; off < 64; off <<= 1) {
-            const int up = __shfl_up(ip, off, 64), uc = __shfl_up(ic, off, 64);
-            if (lane >= off) { ip += up; ic += uc; }
+            const int up = __shfl_up(ip, off, 64);
+            if (lane >= off) ip += up;
         }
-        __shared__ int s_wp[4], s_wc[4];
-        if (lane == 63) { s_wp[wave] = ip; s_wc[wave] = ic; }
+        __shared__ int s_wp[4];
+        if (lane == 63) s_wp[wave] = ip;
         __syncthreads();
-        int bp = 0, bc = 0;
-        for (int w2 = 0; w2 < wave; ++w2) { bp += s_wp[w2]; bc += s_wc[w2]; }
+        int bp = 0;
+        for (int w2 = 0; w2 < wave; ++w2) bp += s_wp[w2];
         bp += ip - sp;  // exclusive prefix of this thread
-        bc += ic - sc;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int e = e0 + j;
-            if (e < E) {
-                p.poff[e] = bp + cp[j];
-                s_poff[e] = bp + cp[j];
-                p.coff[e] = bc + cc[j];
-                p.cnt[e] = s_cnt[e];
-            }
-        }
+        for (int j = 0; j < 4; ++j)
+            if (e0 + j < E) s_poff[e0 + j] = bp + cp[j];
         if (tid == 255) {
-            const int tp = bp + sp, tc = bc + sc;
-            p.poff[E] = tp;
+            const int tp = bp + sp;  // a multiple of MB
             s_poff[E] = tp;
-            p.coff[E] = tc;
             p.totals[0] = tp;
-            p.totals[1] = tc;
+            p.totals[1] = tp / a.MB;
         }
         __syncthreads();
         // padded pair offsets are multiples of MB, so expert e owns chunks
@@ -622,14 +594,16 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i >= H) return;
     // every slot's weight, position and value are requested before the sum
-    // (independent loads in flight together), then summed in slot order
+    // (independent loads in flight together), then summed in slot order;
+    // without a position table (pos null) slot s is pair t * k + s
     double w[kMoeMaxK];
     float y[kMoeMaxK];
 #pragma unroll
     for (int s = 0; s < kMoeMaxK; ++s)
         if (s < k) {
-            w[s] = wts[(unsigned long long)t * k + s];
-            y[s] = YD[(unsigned long long)pos[(unsigned long long)t * k + s] * H + i];
+            const unsigned long long q = (unsigned long long)t * k + s;
+            w[s] = wts[q];
+            y[s] = YD[(unsigned long long)(pos ? pos[q] : q) * H + i];
         }
     double acc = 0.0;
 #pragma unroll
@@ -1240,9 +1214,6 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
         *mags = cv.take<double>(batch * E);
         *ids = cv.take<int>(batch * K);
         *wts = cv.take<double>(batch * K);
-        p->cnt = cv.take<int>(E);
-        p->poff = cv.take<int>(E + 1);
-        p->coff = cv.take<int>(E + 1);
         p->pair_tok = cv.take<int>(max_pairs);
         p->pos = cv.take<int>(batch * K);
         p->totals = cv.take<int>(2);
@@ -1422,16 +1393,17 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
                            (int)max_pairs, act);
         if (hipGetLastError() != hipSuccess) return -4;
     }
+    const bool al_dn = (reinterpret_cast<uintptr_t>(L.down) & 3u) == 0;
     // 6. down
     ma.nm = 1;
     ma.tile = tile_for(H);
     ma.m[0] = fuse_act ? mat(L.down, ds, gd, g, u, yd, H, I) : mat(L.down, ds, gd, act, nullptr, yd, H, I);
-    if (moe_mv_launch(L.down_type, MB, ma, (reinterpret_cast<uintptr_t>(L.down) & 3u) == 0, fuse_act ? 2 : 0,
-                      stream) != hipSuccess)
+    if (moe_mv_launch(L.down_type, MB, ma, al_dn, fuse_act ? 2 : 0, stream) != hipSuccess)
         return -4;
-    // 7. combine
+    // 7. combine (one token: pairs in slot order)
     hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)batch), dim3(256), 0, stream,
-                       yd, (int)H, (int)K, plan.pos, wts, out, (unsigned long long)ldo);
+                       yd, (int)H, (int)K, batch == 1 && MB == 1 ? nullptr : plan.pos, wts, out,
+                       (unsigned long long)ldo);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

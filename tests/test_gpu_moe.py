@@ -105,6 +105,22 @@ def test_moe_other_types(orc, dev, batch):
         _check(orc, layer, host, xs, f"types {types}")
 
 
+@pytest.mark.parametrize("E,H,I,k,types", [
+    (32, 512, 768, 12, (0, 12, 12, 14)),    # twelve slots
+    (24, 256, 512, 16, (0, 12, 12, 14)),    # sixteen slots
+    (16, 256, 2048, 4, (0, 2, 2, 2)),       # two units per lane of a down row (Q4_0, 2048 columns)
+    (16, 512, 256, 6, (0, 13, 13, 11)),     # Q5_K gate/up, Q3_K down
+    (16, 512, 256, 3, (0, 8, 8, 8)),        # Q8_0 throughout, three slots
+])
+def test_moe_single_token_shapes(orc, dev, E, H, I, k, types):
+    """One token (pairs in slot order, combine without the position table):
+    slot counts above eight, rows of two units per lane, other block formats."""
+    rng = np.random.default_rng(E * 1000 + k * 10 + I)
+    layer, host = _layer(orc, rng, E, H, I, k, types=types, seed=E + k + I)
+    xs = orc.normal(1100 + k, H)[None, :]
+    _check(orc, layer, host, xs, f"single token E={E} k={k} types {types}")
+
+
 def test_moe_router_ties(orc, dev):
     """Duplicate router rows: equal logits, the lower expert index ranks first."""
     rng = np.random.default_rng(400)
