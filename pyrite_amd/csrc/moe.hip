@@ -253,7 +253,6 @@ __device__ void moe_route_token(const MoeRouteArgs& a, const int t) {
     const float* x = a.X + (unsigned long long)t * a.ldx;
     __shared__ int s_rank[kMoeMaxE];
     __shared__ double s_tl[kMoeMaxK + 1], s_tb[kMoeMaxK + 1];
-    __shared__ int s_slow;
     __shared__ double s_total;
     __shared__ double s_w[kMoeMaxK];
 
@@ -357,6 +356,7 @@ __device__ void moe_route_token(const MoeRouteArgs& a, const int t) {
     //    probabilities are formed as the reference forms them.  Non-finite
     //    logits keep the (-l, e) order, NaN last.
     // one thread per pair (i, i + 1), i < k, i + 1 < kk
+    bool slow;
     {
         const int np = kk - 1 < k ? kk - 1 : k;
         int bad = 0;
@@ -370,11 +370,8 @@ __device__ void moe_route_token(const MoeRouteArgs& a, const int t) {
                 bad = !(gap > margin) || lb - l0 < -700.0;
             }
         }
-        bad = __syncthreads_or(bad);
-        if (tid == 0) s_slow = bad;
+        slow = __syncthreads_or(bad);  // block-uniform
     }
-    __syncthreads();
-    const bool slow = s_slow;
     if (slow) {
         // every row as the reference computes it (pyrite/kernels/native.c:527-553)
         for (int e = tid; e < E; e += 256) {
@@ -404,7 +401,13 @@ __device__ void moe_route_token(const MoeRouteArgs& a, const int t) {
     //    device's exp (within an ulp of the host's) and a tree total, which
     //    move the weights by fp64 rounding only
     const double peak = s_l[s_top[0]];
-    if (!slow) {
+    if (!slow && a.norm_topk && !nonfinite) {
+        // renormalised weights: p_s / (sum of the k chosen p) = e_s / (sum
+        // of the k chosen e) with e = exp(l - peak), so the softmax total
+        // cancels and only the chosen terms are formed (the same fp64
+        // rounding-level difference as the tree total below)
+        if (tid < k) s_w[tid] = exp(s_l[s_top[tid]] - peak);
+    } else if (!slow) {
         double tot = 0.0;
         for (int e = tid; e < E; e += 256) {
             const double v = exp(s_l[e] - peak);
