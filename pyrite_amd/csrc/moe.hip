@@ -1282,10 +1282,10 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     if (hipGetLastError() != hipSuccess) return -4;
     if (mfma) {
         // 3. fragments of each chunk's tokens; 4. gate and up with silu(gate) * up;
-        // 5. down; 6. combine.  Contiguous item ranges over twice the CUs, row
-        // parts so that about one item per workgroup exists at the likely
-        // chunk count (one per distinct expert; measured on MI355X, fewer and
-        // larger items beat two or more per workgroup).
+        // 5. down; 6. combine.  Contiguous item ranges over at least twice
+        // the CUs (item_grid), row parts so that about one item per workgroup
+        // exists at the likely chunk count (one per distinct expert; measured
+        // on MI355X, fewer and larger items beat two or more per workgroup).
         const int grid = 2 * dev_info().cus;
         const size_t est_chunks = E < batch * K ? E : batch * K;
         hipLaunchKernelGGL(moe_xfrag_kernel, dim3((unsigned)max_chunks), dim3(256), 0, stream, X,
@@ -1307,6 +1307,16 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
             xa.part_rows = (int)pr;
             xa.parts = (int)((rows + pr - 1) / pr);
         };
+        // One workgroup per item wherever the plan's largest chunk count
+        // allows it: with the grid at 2 x CUs, a few chunks more than
+        // estimated gave every workgroup two items (down at 64 tokens: 129
+        // chunks, 516 items on 512 workgroups, 145 us instead of 80).
+        // Workgroups past the actual items return at once.
+        auto item_grid = [&]() {
+            const size_t most = max_chunks * (size_t)xa.parts, cap = 4 * (size_t)dev_info().cus;
+            const size_t g2 = most < cap ? most : cap;
+            return (int)(g2 > (size_t)grid ? g2 : (size_t)grid);
+        };
         xa.W[0] = static_cast<const uint8_t*>(L.gate);
         xa.W[1] = static_cast<const uint8_t*>(L.up);
         xa.slice = gs;
@@ -1317,7 +1327,7 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
         xa.Y = act;
         set_parts(I);
         const bool al_gu2 = ((reinterpret_cast<uintptr_t>(L.gate) | reinterpret_cast<uintptr_t>(L.up)) & 3u) == 0;
-        if (moe_mx_launch(L.gate_type, xa, true, al_gu2, grid, stream) != hipSuccess) return -4;
+        if (moe_mx_launch(L.gate_type, xa, true, al_gu2, item_grid(), stream) != hipSuccess) return -4;
         xa.W[0] = xa.W[1] = static_cast<const uint8_t*>(L.down);
         xa.slice = ds;
         xa.row_bytes = I / gd.bs * gd.bpb;
@@ -1328,8 +1338,8 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
         xa.act = act;
         xa.Y = yd;
         set_parts(H);
-        if (moe_mx_launch(L.down_type, xa, false, (reinterpret_cast<uintptr_t>(L.down) & 3u) == 0, grid, stream) !=
-            hipSuccess)
+        if (moe_mx_launch(L.down_type, xa, false, (reinterpret_cast<uintptr_t>(L.down) & 3u) == 0, item_grid(),
+                          stream) != hipSuccess)
             return -4;
         hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)batch), dim3(256), 0,
                            stream, yd, (int)H, (int)K, plan.pos, wts, out, (unsigned long long)ldo);
