@@ -934,6 +934,10 @@ template <int T, bool AL, int NM, class Done>
 __device__ __forceinline__ void moe_mx_walk(const MoeMxArgs& a, int e, int row_lo, int row_hi, const uint4* frag,
                                             f4v (&acc)[NM][2], Done done) {
     using F = Mx<T>;
+    // unaligned 256-column blocks (Q6_K rows: 210 bytes) as loads at the
+    // spans' own byte addresses: about half the load instructions of dword
+    // loads realigned in registers, each touching fewer cache lines
+    constexpr bool UA = !AL && F::BS == 256;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
     const int nblk = a.cols / F::BS;
     const int ntile = (row_hi - row_lo + kMoeMxRows - 1) / kMoeMxRows;
@@ -948,7 +952,8 @@ __device__ __forceinline__ void moe_mx_walk(const MoeMxArgs& a, int e, int row_l
         for (int h = 0; h < 2; ++h) {
             long long r = (long long)row_lo + (long long)tile * kMoeMxRows + 32 * w + 16 * h + n;
             if (r >= a.rows) r = a.rows - 1;
-            F::template load<AL>(Wm + (unsigned long long)r * a.row_bytes + (size_t)b * F::BPB, g, h ? r1 : r0);
+            F::template load<AL, false, UA>(Wm + (unsigned long long)r * a.row_bytes + (size_t)b * F::BPB, g,
+                                            h ? r1 : r0);
         }
     };
     typename F::Raw ra[kMoeMxPF], rb[kMoeMxPF];
