@@ -121,6 +121,31 @@ def test_moe_single_token_shapes(orc, dev, E, H, I, k, types):
     _check(orc, layer, host, xs, f"single token E={E} k={k} types {types}")
 
 
+def test_moe_many_items_per_workgroup(orc, dev):
+    """300 tokens over 64 experts: the down launch has more items (about 1200:
+    chunks x 4 row parts) than workgroups (at most 4 per CU), so workgroups
+    walk contiguous item ranges of two or more, reusing a chunk's staged
+    fragments across its parts.  Every 7th token and the last are checked."""
+    rng = np.random.default_rng(5300)
+    layer, host = _layer(orc, rng, 64, 512, 256, 8, seed=5301)
+    xs = np.stack([orc.normal(5400 + b, 512) for b in range(300)])
+    from pyrite_amd import device
+    announce("moe", "many items", "E=64", "H=512", "I=256", "k=8", "batch=300")
+    out, ids, wts = device.moe_ffn(layer, torch.from_numpy(np.ascontiguousarray(xs)).to("cuda:0"))
+    torch.cuda.synchronize()
+    out, ids, wts = out.cpu().numpy(), ids.cpu().numpy(), wts.cpu().numpy()
+    router, gate, up, down = host
+    for b in list(range(0, 300, 7)) + [299]:
+        ref, rids, rw, _ = orc.moe_ffn(router, layer.router_type, gate, layer.gate_type, up, layer.up_type,
+                                       down, layer.down_type, layer.n_experts, layer.hidden, layer.inter,
+                                       layer.k, xs[b].astype(np.float64), layer.norm_topk_prob, layer.scale)
+        assert list(ids[b]) == list(rids), f"b={b}: ids {list(ids[b])} != {list(rids)}"
+        np.testing.assert_allclose(wts[b], rw, rtol=2e-7, atol=1e-30, err_msg=f"b={b} weights")
+        scale = float(np.max(np.abs(ref)))
+        err = float(np.max(np.abs(out[b].astype(np.float64) - ref)))
+        assert err <= 1e-4 * scale + 1e-30, f"b={b}: max err {err} vs scale {scale}"
+
+
 def test_moe_router_ties(orc, dev):
     """Duplicate router rows: equal logits, the lower expert index ranks first."""
     rng = np.random.default_rng(400)
