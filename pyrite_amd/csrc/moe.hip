@@ -936,7 +936,7 @@ __device__ __forceinline__ void moe_mx_walk(const MoeMxArgs& a, int e, int row_l
     using F = Mx<T>;
     // unaligned 256-column blocks (Q6_K rows: 210 bytes) as loads at the
     // spans' own byte addresses: about half the load instructions of dword
-    // loads realigned in registers, each touching fewer cache lines
+    // loads realigned in registers (the cache lines touched stay the same)
     constexpr bool UA = !AL && F::BS == 256;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, g = lane >> 4, n = lane & 15;
     const int nblk = a.cols / F::BS;
