@@ -208,6 +208,7 @@ struct MoePlan {
     int* pos;        // [batch * k] padded pair index of (token, slot)
     int* totals;     // [2]: padded pairs, chunks
     int* chunk_e;    // [chunks] expert of each chunk; chunk c holds padded pairs [c * MB, (c + 1) * MB)
+    unsigned* amax;  // [padded pairs] zeroed with the plan (matrix-core experts), or null
 };
 
 struct MoeRouteArgs {
@@ -535,6 +536,8 @@ __device__ void moe_route_token(const MoeRouteArgs& a, const int t) {
     __syncthreads();
     for (int e = tid; e < E; e += 256)
         for (int q = s_cnt[e]; q < s_poff[e + 1]; ++q) p.pair_tok[q] = -1;
+    if (p.amax)  // the gate/up launch folds each pair's largest |act| into it
+        for (int q = tid; q < s_poff[E]; q += 256) p.amax[q] = 0u;
     if (tid == 0) st_dev(a.arrive, 0u);
 }
 
@@ -815,12 +818,11 @@ static bool moe_fused_ok(int type, int MB, size_t cols) {
 // row 2t + p = fp16 hi (p = 0) / lo (p = 1) part of token t, each token
 // scaled by the power of two 2^-e_t that brings its largest finite |x| into
 // [2^14, 2^15), the results multiplied back by 2^e_t).
-//   moe_xfrag_kernel  one workgroup per chunk: gathers the chunk's tokens and
-//                     writes their A fragments (in the gate/up format's
-//                     K-slot map) and exponents once
-//   moe_gu_kernel     items (chunk, row part): gate and up rows of the part
-//                     against the chunk's fragments (copied to LDS), writes
-//                     silu(gate) * up and the pair's largest finite |act|
+//   moe_gu_kernel     items (chunk, row part): gathers the chunk's tokens as
+//                     A fragments in LDS (moe_stage_frags, in the gate/up
+//                     format's K-slot map), multiplies the part's gate and
+//                     up rows, writes silu(gate) * up and folds the pair's
+//                     largest finite |act| (zeroed with the routing plan)
 //   moe_dn_kernel     items (chunk, row part): down rows against the chunk's
 //                     activations (staged as fragments from act)
 // A workgroup takes a contiguous range of items (consecutive items share a
@@ -838,8 +840,10 @@ struct MoeMxArgs {
     unsigned long long row_bytes;
     int rows, cols;
     int parts, part_rows;       // row parts per chunk; rows per part (a multiple of kMoeMxRows)
-    const uint4* xf;            // [chunk][cols / 32][4][16] fragments (moe_gu_kernel)
-    const int* xe;              // [chunk][kMoeMxTok] exponents (moe_gu_kernel)
+    const float* X;             // the caller's tokens [batch][ldx] (moe_gu_kernel)
+    unsigned long long ldx;
+    const int* pair_tok;        // token of each padded pair, -1 for padding
+    int kmode;                  // K-slot map of the gate/up format (mx_kcol)
     const float* act;           // [pairs][cols] silu(gate) * up (moe_dn_kernel)
     unsigned* amax;             // [pairs] largest finite |act| (ordered uint bits)
     float* Y;                   // moe_gu_kernel: act [pairs][rows]; moe_dn_kernel: [pairs][rows]
@@ -855,27 +859,24 @@ __device__ __forceinline__ float moe_act(float g, float u) {
 
 // One workgroup per chunk: the gathered tokens' fragments, exponents, and the
 // chunk's act maxima cleared for moe_gu_kernel.
-__global__ __launch_bounds__(256) void moe_xfrag_kernel(const float* X, unsigned long long ldx, int cols,
-                                                        const int* pair_tok, const int* totals, int kmode,
-                                                        uint4* xf, int* xe,
-                                                        unsigned* amax) {
-    __shared__ unsigned tok_max[kMoeMxTok];
-    __shared__ int tok_id[kMoeMxTok];
-    const int chunk = blockIdx.x;
-    if (chunk >= totals[1]) return;
-    const int pair0 = chunk * kMoeMxTok;
+// A chunk's tokens as A fragments in LDS (frag[(step * 4 + group) * 16 +
+// 2 t + part], the K-slot map kmode) and each token's exponent (tok_e): the
+// largest finite |x| of token t, then x * 2^-e_t split into fp16 hi and lo
+// parts.  Padding pairs are zeros.  The whole workgroup calls it; it ends
+// with a barrier.
+__device__ void moe_stage_frags(const MoeMxArgs& a, int pair0, uint4* frag, int* tok_e, unsigned* tok_max,
+                                int* tok_id) {
     const int tid = threadIdx.x;
     if (tid < kMoeMxTok) {
         tok_max[tid] = 0u;
-        tok_id[tid] = pair_tok[pair0 + tid];
-        amax[pair0 + tid] = 0u;
+        tok_id[tid] = a.pair_tok[pair0 + tid];
     }
     __syncthreads();
     // item idx = (step st, K-slot group gg, token t): 8 columns of token t;
     // each thread takes items tid + 256 j, 8 at a time, every load of a batch
     // issued before any is used
     constexpr int kB = 8;
-    const int steps = cols >> 5, count = steps * 4 * kMoeMxTok;
+    const int steps = a.cols >> 5, count = steps * 4 * kMoeMxTok;
     auto load_batch = [&](int base, float (&v)[kB][8]) {
         float4 q[kB][2];
 #pragma unroll
@@ -884,7 +885,7 @@ __global__ __launch_bounds__(256) void moe_xfrag_kernel(const float* X, unsigned
             const int t = idx % kMoeMxTok, gg = (idx / kMoeMxTok) & 3, st = idx / (4 * kMoeMxTok);
             const int tok = idx < count ? tok_id[t] : -1;
             // padding pairs and items past the end read token 0's first columns (not used)
-            const float* p = X + (tok < 0 ? 0ull : (unsigned long long)tok * ldx + mx_kcol(kmode, st, gg));
+            const float* p = a.X + (tok < 0 ? 0ull : (unsigned long long)tok * a.ldx + mx_kcol(a.kmode, st, gg));
             q[j][0] = ld_x4(p);
             q[j][1] = ld_x4(p + 4);
         }
@@ -908,7 +909,6 @@ __global__ __launch_bounds__(256) void moe_xfrag_kernel(const float* X, unsigned
         }
     }
     __syncthreads();
-    uint4* out = xf + (size_t)chunk * steps * 64;
     for (int base = 0; base < count; base += 256 * kB) {
         float v[kB][8];
         load_batch(base, v);
@@ -919,11 +919,12 @@ __global__ __launch_bounds__(256) void moe_xfrag_kernel(const float* X, unsigned
             const int t = idx % kMoeMxTok, gg = (idx / kMoeMxTok) & 3, st = idx / (4 * kMoeMxTok);
             uint4 h, l;
             split8(v[j], norm_exp(__uint_as_float(tok_max[t])), h, l);
-            out[(st * 4 + gg) * 16 + 2 * t] = h;
-            out[(st * 4 + gg) * 16 + 2 * t + 1] = l;
+            frag[(st * 4 + gg) * 16 + 2 * t] = h;
+            frag[(st * 4 + gg) * 16 + 2 * t + 1] = l;
         }
     }
-    if (tid < kMoeMxTok) xe[chunk * kMoeMxTok + tid] = norm_exp(__uint_as_float(tok_max[tid]));
+    if (tid < kMoeMxTok) tok_e[tid] = norm_exp(__uint_as_float(tok_max[tid]));
+    __syncthreads();
 }
 
 // The block sequence of one wave over a row part of one or two matrices that
@@ -1024,8 +1025,9 @@ __global__ __launch_bounds__(256, 2) void moe_gu_kernel(const MoeMxArgs a) {
     uint4* frag = reinterpret_cast<uint4*>(smem);
     float* res = smem + (size_t)a.cols * 8;  // [part_rows][kMoeMxTok]
     __shared__ int tok_e[kMoeMxTok];
+    __shared__ unsigned tok_max[kMoeMxTok];
+    __shared__ int tok_id[kMoeMxTok];
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, g = lane >> 4, n = lane & 15;
-    const int steps = a.cols >> 5;
     long long it0, it1;
     moe_item_range((long long)a.totals[1] * a.parts, it0, it1);
     int staged = -1;
@@ -1035,10 +1037,7 @@ __global__ __launch_bounds__(256, 2) void moe_gu_kernel(const MoeMxArgs a) {
         const int pair0 = chunk * kMoeMxTok;
         __syncthreads();  // the previous item's waves are done with the fragments and results
         if (chunk != staged) {
-            const uint4* src = a.xf + (size_t)chunk * steps * 64;
-            for (int i = tid; i < steps * 64; i += 256) frag[i] = src[i];
-            if (tid < kMoeMxTok) tok_e[tid] = a.xe[chunk * kMoeMxTok + tid];
-            __syncthreads();
+            moe_stage_frags(a, pair0, frag, tok_e, tok_max, tok_id);
             staged = chunk;
         }
         const int row_lo = part * a.part_rows;
@@ -1210,13 +1209,9 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
 
     Carver c{nullptr};
     const size_t max_chunks = mfma ? max_pairs / kMoeMxTok : 0;
-    uint4* xf = nullptr;
-    int* xe = nullptr;
     unsigned* amax = nullptr;
     auto layout = [&](Carver& cv, double** logits, double** mags, int** ids, double** wts, MoePlan* p, float** xg,
                       float** g, float** u, float** act, float** yd) {
-        xf = cv.take<uint4>(max_chunks * (H / 32) * 64);
-        xe = cv.take<int>(max_chunks * kMoeMxTok);
         amax = cv.take<unsigned>(mfma ? max_pairs : 0);
         *logits = cv.take<double>(batch * E);
         *mags = cv.take<double>(batch * E);
@@ -1271,6 +1266,7 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
     ra.ids_out = ids_out;
     ra.batch = (int)batch;
     ra.arrive = static_cast<unsigned int*>(ws->arrive);
+    plan.amax = mfma ? amax : nullptr;  // zeroed by the plan only for the matrix-core experts
     ra.plan = plan;
     if (batch <= kMoeFusedRouteBatch) {
         // counters 1 .. batch of the zeroed arrival block (0 is the token counter)
@@ -1293,16 +1289,14 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
         // on MI355X, fewer and larger items beat two or more per workgroup).
         const int grid = 2 * dev_info().cus;
         const size_t est_chunks = E < batch * K ? E : batch * K;
-        hipLaunchKernelGGL(moe_xfrag_kernel, dim3((unsigned)max_chunks), dim3(256), 0, stream, X,
-                           (unsigned long long)ldx, (int)H, plan.pair_tok, plan.totals,
-                           moe_kmode(L.gate_type), xf, xe, amax);
-        if (hipGetLastError() != hipSuccess) return -4;
         MoeMxArgs xa;
         xa.chunk_e = plan.chunk_e;
         xa.totals = plan.totals;
         xa.E = (int)E;
-        xa.xf = xf;
-        xa.xe = xe;
+        xa.X = X;
+        xa.ldx = ldx;
+        xa.pair_tok = plan.pair_tok;
+        xa.kmode = moe_kmode(L.gate_type);
         xa.amax = amax;
         auto set_parts = [&](size_t rows) {
             size_t parts = ((size_t)grid + est_chunks - 1) / est_chunks;
@@ -1338,8 +1332,6 @@ int moe_ffn_launch(const MoeLayer& L, const float* X, size_t ldx, float* out, si
         xa.row_bytes = I / gd.bs * gd.bpb;
         xa.rows = (int)H;
         xa.cols = (int)I;
-        xa.xf = nullptr;
-        xa.xe = nullptr;
         xa.act = act;
         xa.Y = yd;
         set_parts(H);
