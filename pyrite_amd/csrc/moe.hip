@@ -827,11 +827,14 @@ static bool moe_fused_ok(int type, int MB, size_t cols) {
 //                     activations (staged as fragments from act)
 // A workgroup takes a contiguous range of items (consecutive items share a
 // chunk); its 4 waves walk the part in 128-row tiles (two 16-row MFMA tiles
-// per wave) with kMoeMxPF blocks of weights in flight per wave.
+// per wave) with kMoeMxPF (gate/up) or kMoeDnPF (down) blocks of weights in
+// flight per wave.
 constexpr int kMoeMxTok = 8;
 constexpr int kMoeMxRows = 128;
 constexpr int kMoeMxMaxCols = 3072;  // activation fragments of a chunk: cols * 32 bytes of LDS
-constexpr int kMoeMxPF = 3;          // blocks per wave in flight
+constexpr int kMoeMxPF = 3;          // blocks per wave in flight (gate/up: its LDS allows two workgroups per CU)
+constexpr int kMoeDnPF = 2;          // down: two blocks keep it at 147 VGPRs, three workgroups per CU
+                                     // (three blocks: 181 VGPRs, two; 64 tokens: 75 against 78.5 us)
 constexpr int kMoeMxMaxPart = 512;   // rows per part at most (results buffered in LDS)
 
 struct MoeMxArgs {
@@ -931,7 +934,7 @@ __device__ void moe_stage_frags(const MoeMxArgs& a, int pair0, uint4* frag, int*
 // share the staged fragments: q runs over (tile, matrix, block); raw[p] holds
 // block q0 + p.  acc[j] collects matrix j of the current tile; done(tile)
 // is called after the last block of each tile.
-template <int T, bool AL, int NM, class Done>
+template <int T, bool AL, int NM, int PF, class Done>
 __device__ __forceinline__ void moe_mx_walk(const MoeMxArgs& a, int e, int row_lo, int row_hi, const uint4* frag,
                                             f4v (&acc)[NM][2], Done done) {
     using F = Mx<T>;
@@ -957,15 +960,15 @@ __device__ __forceinline__ void moe_mx_walk(const MoeMxArgs& a, int e, int row_l
                                             h ? r1 : r0);
         }
     };
-    typename F::Raw ra[kMoeMxPF], rb[kMoeMxPF];
+    typename F::Raw ra[PF], rb[PF];
 #pragma unroll
-    for (int p = 0; p < kMoeMxPF; ++p) {
+    for (int p = 0; p < PF; ++p) {
         load_q(p, ra[p], rb[p]);
         asm volatile("" ::: "memory");
     }
-    for (int q0 = 0; q0 < nq; q0 += kMoeMxPF) {
+    for (int q0 = 0; q0 < nq; q0 += PF) {
 #pragma unroll
-        for (int p = 0; p < kMoeMxPF; ++p) {
+        for (int p = 0; p < PF; ++p) {
             const int q = q0 + p;
             if (q < nq) {
                 const int tile = q / per_tile, rem = q - tile * per_tile;
@@ -1001,7 +1004,7 @@ __device__ __forceinline__ void moe_mx_walk(const MoeMxArgs& a, int e, int row_l
                 }
                 if (rem == per_tile - 1) done(tile);
             }
-            load_q(q + kMoeMxPF, ra[p], rb[p]);
+            load_q(q + PF, ra[p], rb[p]);
             // keep the refills in slot order: loads complete in order, so a
             // slot refilled after a later one would make its wait cover both
             asm volatile("" ::: "memory");
@@ -1046,7 +1049,7 @@ __global__ __launch_bounds__(256, 2) void moe_gu_kernel(const MoeMxArgs a) {
         f4v acc[2][2];
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[j][0] = acc[j][1] = f4v{0.f, 0.f, 0.f, 0.f};
-        moe_mx_walk<T, AL, 2>(a, e, row_lo, row_hi, frag, acc, [&](int tile) {
+        moe_mx_walk<T, AL, 2, kMoeMxPF>(a, e, row_lo, row_hi, frag, acc, [&](int tile) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int lr = tile * kMoeMxRows + 32 * w + 16 * h + n;  // row within the part
@@ -1077,7 +1080,7 @@ __global__ __launch_bounds__(256, 2) void moe_gu_kernel(const MoeMxArgs a) {
 }
 
 template <int T, bool AL>
-__global__ __launch_bounds__(256, 2) void moe_dn_kernel(const MoeMxArgs a) {
+__global__ __launch_bounds__(256, 3) void moe_dn_kernel(const MoeMxArgs a) {
     extern __shared__ float smem[];
     uint4* frag = reinterpret_cast<uint4*>(smem);
     float* res = smem + (size_t)a.cols * 8;  // [part_rows][kMoeMxTok]
@@ -1113,7 +1116,7 @@ __global__ __launch_bounds__(256, 2) void moe_dn_kernel(const MoeMxArgs a) {
         const int te0 = tok_e[2 * g], te1 = tok_e[2 * g + 1];
         f4v acc[1][2];
         acc[0][0] = acc[0][1] = f4v{0.f, 0.f, 0.f, 0.f};
-        moe_mx_walk<T, AL, 1>(a, e, row_lo, row_hi, frag, acc, [&](int tile) {
+        moe_mx_walk<T, AL, 1, kMoeDnPF>(a, e, row_lo, row_hi, frag, acc, [&](int tile) {
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int lr = tile * kMoeMxRows + 32 * w + 16 * h + n;
